@@ -1,0 +1,204 @@
+/*
+ * reef_hip: int8 attention for AMD MI355X (gfx950), C ABI.
+ *
+ * Drop-in device back end for the Reef engine's attention and quantization
+ * operators (inference-engine/reference/cpp/include/inference_engine/). Every
+ * entry point names the engine function whose arithmetic it follows, in the
+ * way the engine's kernel ABI does (coral/include/reef_kernels/kernels.hpp:3-16):
+ *
+ *   - The caller owns every buffer; pointers are device pointers, arrays are
+ *     row-major, and the innermost (head_dim / width) dimension is contiguous.
+ *     Nothing here allocates or keeps hidden state, so calls are stream-ordered
+ *     and re-entrant (kernels.hpp:13-14).
+ *   - Where the engine throws, an entry point returns a status instead
+ *     (kernels.hpp has no error path; host_if.hpp:24-30 uses status codes). All
+ *     shape and argument checks run on the host before any launch.
+ *   - Conditions only the device can see (non-finite values, out-of-range page
+ *     numbers) set bits in an optional caller-owned device word (status_word);
+ *     reef_read_status_word() waits for the stream and maps the word to a
+ *     status. The C++ wrapper attention.hpp turns statuses into the engine's
+ *     exception types.
+ *
+ * Scores follow the engine's W8A8 dequantization order
+ * (operator/linear.hpp:125-127): s = float(int32 q.k) * (s_q * s_k), times
+ * softmax_scale (1 reproduces the engine's unscaled attend_head,
+ * attention.hpp:102-106; 1/sqrt(head_dim) is scaled dot-product attention).
+ */
+#ifndef REEF_HIP_ATTENTION_H
+#define REEF_HIP_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum reef_status {
+    REEF_OK = 0,
+    /* engine: std::invalid_argument for shapes and masks
+     * (activation.hpp:178-181, 204-207; attention.hpp:293-318). */
+    REEF_INVALID_ARGUMENT = 1,
+    /* engine: std::invalid_argument from quantize_int8 (quant.hpp:72-74). */
+    REEF_NON_FINITE_INPUT = 2,
+    /* engine: std::length_error for the KV cache (attention.hpp:321-327). */
+    REEF_CAPACITY = 3,
+    /* a HIP runtime call failed. */
+    REEF_HIP_ERROR = 4,
+    /* well-formed but outside what the kernels implement (e.g. head_dim). */
+    REEF_UNSUPPORTED = 5
+} reef_status;
+
+/* Bits set in a status word by the kernels. */
+#define REEF_STATUS_BIT_NON_FINITE 0x1u
+#define REEF_STATUS_BIT_BAD_PAGE 0x2u
+#define REEF_STATUS_BIT_BAD_LENGTH 0x4u
+
+typedef enum reef_scale_granularity {
+    REEF_SCALE_PER_TENSOR = 0, /* one scale: scales[0] */
+    REEF_SCALE_PER_HEAD = 1,   /* scales[head], over batch and tokens */
+    REEF_SCALE_PER_TOKEN = 2   /* scales[(b * heads + head) * tokens + t] */
+} reef_scale_granularity;
+
+/* Element strides of a [batch, heads, tokens, head_dim] tensor whose head_dim
+ * is contiguous. NULL means the packed layout {H*S*D, S*D, D}. The engine keeps
+ * heads as [1, heads, len, head_dim] (attention.hpp:49-68); a projection
+ * output [len, heads * head_dim] is {0, D, H*D}. */
+typedef struct reef_strides {
+    int64_t batch, head, token;
+} reef_strides;
+
+/* ---------------------------------------------------------------------------
+ * Quantization (quant.hpp): scale = max|x| / 127 (1 when max is 0), code =
+ * clamp(nearbyint(x / scale), -127, 127), IEEE division, ties to even. The
+ * codes and scales are bit-identical to the engine's.
+ */
+
+/* The quant.hpp rule with one scale over all n values. scale: 1 float. */
+reef_status reef_quantize_int8_per_tensor(const float *x, int64_t n, int8_t *q, float *scale,
+                                          uint32_t *status_word, hipStream_t stream);
+
+/* x: [B, H, S, D] with x_strides (NULL = packed); q: packed [B, H, S, D];
+ * scales: [H], each over x[:, h, :, :]. */
+reef_status reef_quantize_int8_per_head(const float *x, int64_t batch, int64_t heads,
+                                        int64_t tokens, int64_t head_dim,
+                                        const reef_strides *x_strides, int8_t *q, float *scales,
+                                        uint32_t *status_word, hipStream_t stream);
+
+/* quantize_rows (quant.hpp:112-133), the per-token quantizer of the W8A8
+ * linear (linear.hpp:120): rows of width values, row r at x + r * row_stride;
+ * q packed [rows, width]; scales [rows]. */
+reef_status reef_quantize_int8_per_token(const float *x, int64_t rows, int64_t width,
+                                         int64_t row_stride, int8_t *q, float *scales,
+                                         uint32_t *status_word, hipStream_t stream);
+
+/* Dequantize: x[i] = float(q[i]) * scale[i / group] (group = width for
+ * per-token rows, n for per-tensor). */
+reef_status reef_dequantize_int8(const int8_t *q, int64_t n, int64_t group, const float *scales,
+                                 float *x, hipStream_t stream);
+
+/* Waits for the stream, reads a status word written by the kernels and maps
+ * it: 0 -> REEF_OK, NON_FINITE -> REEF_NON_FINITE_INPUT, page/length bits ->
+ * REEF_INVALID_ARGUMENT. Clears the word afterwards when clear != 0. */
+reef_status reef_read_status_word(uint32_t *status_word, int clear, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Attention over int8 Q/K/V with an fp32 softmax and fp32 output.
+ */
+
+/* Attention flags. */
+#define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts */
+
+typedef struct reef_attention_params {
+    int64_t batch, q_heads, kv_heads; /* q head h reads kv head h / (q_heads / kv_heads) */
+    int64_t q_len, kv_len, head_dim;  /* head_dim 64 or 128 */
+    int64_t query_start; /* position of query row 0; engine: kv_len - q_len (attention.hpp:415) */
+    int64_t window;      /* 0: GlobalAttention; > 0: LocalAttention window (attention.hpp:223-261) */
+    float softmax_scale;
+    int32_t q_granularity;  /* reef_scale_granularity of q_scales */
+    int32_t kv_granularity; /* reef_scale_granularity of k_scales and v_scales */
+    uint32_t flags;
+} reef_attention_params;
+
+/* Prefill / general attention: Attention::context (attention.hpp:374-432) for
+ * every (batch, head) in one launch; per head, attend_head (:117-123) with
+ * causal_visibility (:82-100). q [B, Hq, q_len, D], k and v [B, Hkv, kv_len, D],
+ * out fp32 [B, Hq, q_len, D], each with optional strides. Requires
+ * query_start + q_len <= kv_len, so that every row sees a key (the engine
+ * throws for a row with none, activation.hpp:204-207). */
+reef_status reef_attention_prefill_int8(const reef_attention_params *p, const int8_t *q,
+                                        const reef_strides *q_strides, const int8_t *k,
+                                        const reef_strides *k_strides, const int8_t *v,
+                                        const reef_strides *v_strides, const float *q_scales,
+                                        const float *k_scales, const float *v_scales, float *out,
+                                        const reef_strides *out_strides, hipStream_t stream);
+
+/* Bit-exact hook: the int32 score accumulators q . k^T (tensor.hpp:210-246
+ * with int8 inputs and int32 sums), computed by the same MFMA tile code as the
+ * prefill kernel. acc: [B, Hq, q_len, kv_len] int32. Packed q and k. */
+reef_status reef_qk_scores_i32(const int8_t *q, const int8_t *k, int64_t batch, int64_t q_heads,
+                               int64_t kv_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,
+                               int32_t *acc, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Decode over an int8 KV cache (one query token per sequence), split across
+ * workgroups along the keys, partial results combined by log-sum-exp.
+ *
+ * KV cache format (int8 values, fp32 per-token-per-head scales). The cache is
+ * cut into pages of 16 tokens. A K page is [16, D] (token-major, like the
+ * engine's KvCache rows, attention.hpp:64-68). A V page is stored transposed,
+ * [D, 16]: each of its D rows holds one channel of the 16 tokens, which is the
+ * operand layout of the P.V matrix instruction. reef_kv_pack_v_pages() converts
+ * token-major values into this layout and reef_kv_append_int8() writes it.
+ *
+ *   contiguous: k_cache [B, Hkv, L, D]; v_cache [B, Hkv, L/16, D, 16];
+ *               k_scales, v_scales [B, Hkv, L]; L = max_context, a multiple of 16.
+ *   paged:      k_pages [P, Hkv, 16, D]; v_pages [P, Hkv, D, 16];
+ *               k_scale_pages, v_scale_pages [P, Hkv, 16];
+ *               block_table [B, max_blocks_per_seq] int32 page numbers.
+ * q: [B, Hq, D] int8 with q_scales by q_granularity (PER_TOKEN: [B, Hq]);
+ * out: [B, Hq, D] fp32. context_lens: [B] int32 on the device (NULL: every
+ * sequence holds max_context tokens). Query b sits at position
+ * context_lens[b] - 1 and sees all earlier keys (or the last window).
+ * A sequence whose length is outside [1, max_context], or a page number outside
+ * [0, P), sets a status-word bit and yields zeros for that sequence.
+ */
+typedef struct reef_decode_params {
+    int64_t batch, q_heads, kv_heads, head_dim; /* head_dim 64 or 128 */
+    int64_t max_context;  /* tokens per sequence the cache can hold */
+    int64_t window;       /* 0: global */
+    float softmax_scale;
+    int32_t q_granularity;
+    int32_t num_splits;   /* key-range splits per sequence; 0: library choice */
+    uint32_t flags;
+} reef_decode_params;
+
+/* Bytes of device workspace the decode entry points need for params. */
+size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p);
+
+reef_status reef_attention_decode_int8(const reef_decode_params *p, const int8_t *q,
+                                       const float *q_scales, const int8_t *k_cache,
+                                       const int8_t *v_cache, const float *k_scales,
+                                       const float *v_scales, const int32_t *context_lens,
+                                       float *out, void *workspace, size_t workspace_bytes,
+                                       uint32_t *status_word, hipStream_t stream);
+
+reef_status reef_attention_decode_int8_paged(
+    const reef_decode_params *p, const int8_t *q, const float *q_scales, const int8_t *k_pages,
+    const int8_t *v_pages, const float *k_scale_pages, const float *v_scale_pages,
+    const int32_t *block_table, int64_t max_blocks_per_seq, int64_t num_pages,
+    const int32_t *context_lens, float *out, void *workspace, size_t workspace_bytes,
+    uint32_t *status_word, hipStream_t stream);
+
+/* Token-major values [pages * 16, D] (page-contiguous) -> transposed pages
+ * [pages, D, 16]. */
+reef_status reef_kv_pack_v_pages(const int8_t *v_tokens, int64_t pages, int64_t head_dim,
+                                 int8_t *v_pages, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REEF_HIP_ATTENTION_H */

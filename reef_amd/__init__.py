@@ -1,0 +1,375 @@
+"""reef_amd: int8 attention for AMD MI355X behind the reef_hip C ABI.
+
+Host-side mirror of the Reef engine's quantization and attention operators
+(inference-engine/reference/cpp/include/inference_engine/quant.hpp and
+operator/attention.hpp), running on the HIP kernels of libreef_hip.so through
+its C ABI (include/reef_hip/attention.h). Tensors are torch tensors on the GPU;
+torch only provides device memory and the current stream. There is no CPU
+fallback: without the built library every call raises.
+
+Errors follow the engine: shape and argument errors raise InvalidArgument (a
+ValueError, as the engine's std::invalid_argument), non-finite input raises
+NonFiniteInput (also a ValueError, quant.hpp:72-74), cache capacity raises
+CapacityError (an IndexError, the engine's std::length_error).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libreef_hip.so")
+
+OK, INVALID_ARGUMENT, NON_FINITE_INPUT, CAPACITY, HIP_ERROR, UNSUPPORTED = range(6)
+PER_TENSOR, PER_HEAD, PER_TOKEN = 0, 1, 2
+ATTN_PRECISE_PV = 0x1
+PAGE = 16
+
+EXPORTS = [
+    "reef_quantize_int8_per_tensor", "reef_quantize_int8_per_head",
+    "reef_quantize_int8_per_token", "reef_dequantize_int8", "reef_read_status_word",
+    "reef_attention_prefill_int8", "reef_qk_scores_i32",
+    "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
+    "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages",
+]
+
+
+class ReefError(RuntimeError):
+    pass
+
+
+class InvalidArgument(ReefError, ValueError):
+    pass
+
+
+class NonFiniteInput(ReefError, ValueError):
+    pass
+
+
+class CapacityError(ReefError, IndexError):
+    pass
+
+
+class HipError(ReefError):
+    pass
+
+
+class Unsupported(ReefError, NotImplementedError):
+    pass
+
+
+_ERRORS = {INVALID_ARGUMENT: InvalidArgument, NON_FINITE_INPUT: NonFiniteInput,
+           CAPACITY: CapacityError, HIP_ERROR: HipError, UNSUPPORTED: Unsupported}
+
+
+class Strides(C.Structure):
+    _fields_ = [("batch", C.c_int64), ("head", C.c_int64), ("token", C.c_int64)]
+
+
+class AttentionParams(C.Structure):
+    _fields_ = [("batch", C.c_int64), ("q_heads", C.c_int64), ("kv_heads", C.c_int64),
+                ("q_len", C.c_int64), ("kv_len", C.c_int64), ("head_dim", C.c_int64),
+                ("query_start", C.c_int64), ("window", C.c_int64),
+                ("softmax_scale", C.c_float), ("q_granularity", C.c_int32),
+                ("kv_granularity", C.c_int32), ("flags", C.c_uint32)]
+
+
+class DecodeParams(C.Structure):
+    _fields_ = [("batch", C.c_int64), ("q_heads", C.c_int64), ("kv_heads", C.c_int64),
+                ("head_dim", C.c_int64), ("max_context", C.c_int64), ("window", C.c_int64),
+                ("softmax_scale", C.c_float), ("q_granularity", C.c_int32),
+                ("num_splits", C.c_int32), ("flags", C.c_uint32)]
+
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_SIGS = {
+    "reef_quantize_int8_per_tensor": [_P, _I64, _P, _P, _P, _P],
+    "reef_quantize_int8_per_head": [_P, _I64, _I64, _I64, _I64, C.POINTER(Strides), _P, _P, _P,
+                                    _P],
+    "reef_quantize_int8_per_token": [_P, _I64, _I64, _I64, _P, _P, _P, _P],
+    "reef_dequantize_int8": [_P, _I64, _I64, _P, _P, _P],
+    "reef_read_status_word": [_P, C.c_int, _P],
+    "reef_attention_prefill_int8": [C.POINTER(AttentionParams), _P, C.POINTER(Strides), _P,
+                                    C.POINTER(Strides), _P, C.POINTER(Strides), _P, _P, _P, _P,
+                                    C.POINTER(Strides), _P],
+    "reef_qk_scores_i32": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "reef_attention_decode_workspace_bytes": [C.POINTER(DecodeParams)],
+    "reef_attention_decode_int8": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   C.c_size_t, _P, _P],
+    "reef_attention_decode_int8_paged": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P,
+                                         _I64, _I64, _P, _P, _P, C.c_size_t, _P, _P],
+    "reef_kv_pack_v_pages": [_P, _I64, _I64, _P, _P],
+}
+
+_lib_handle = None
+
+
+def lib() -> C.CDLL:
+    """The loaded libreef_hip.so. Raises if it has not been built."""
+    global _lib_handle
+    if _lib_handle is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with python -m reef_amd._build")
+        handle = C.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = C.c_size_t if name.endswith("_bytes") else C.c_int
+        _lib_handle = handle
+    return _lib_handle
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise _ERRORS.get(status, ReefError)(f"{what}: reef status {status}")
+
+
+# --- torch plumbing -------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream():
+    return C.c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _require(t, dtype, name):
+    torch = _torch()
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise InvalidArgument(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise InvalidArgument(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _strides4(t):
+    """Strides of a [B, H, S, D] tensor with a contiguous last dimension."""
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise InvalidArgument("expected [batch, heads, tokens, head_dim] with contiguous head_dim")
+    return Strides(t.stride(0), t.stride(1), t.stride(2))
+
+
+class StatusWord:
+    """A device status word the kernels flag non-finite input and bad pages in."""
+
+    def __init__(self, device=None):
+        torch = _torch()
+        self.tensor = torch.zeros(1, dtype=torch.int32, device=device or "cuda")
+
+    @property
+    def ptr(self):
+        return _ptr(self.tensor)
+
+    def check(self, what: str) -> None:
+        check(lib().reef_read_status_word(self.ptr, 1, _stream()), what)
+
+
+# --- quantization (quant.hpp) ---------------------------------------------------------
+
+def quantize_per_tensor(x, status: StatusWord | None = None):
+    """One scale for the whole tensor (the quant.hpp rule); returns (int8, scale[1])."""
+    torch = _torch()
+    _require(x, torch.float32, "x")
+    x = x.contiguous()
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(1, dtype=torch.float32, device=x.device)
+    own = status or StatusWord(x.device)
+    check(lib().reef_quantize_int8_per_tensor(_ptr(x), x.numel(), _ptr(q), _ptr(s), own.ptr,
+                                              _stream()), "quantize_per_tensor")
+    if status is None:
+        own.check("quantize_per_tensor requires finite values")
+    return q, s
+
+
+def quantize_per_head(x, status: StatusWord | None = None):
+    """x [B, H, S, D] (any strides, contiguous D); one scale per head over batch and
+    tokens. Returns packed int8 [B, H, S, D] and scales [H]."""
+    torch = _torch()
+    _require(x, torch.float32, "x")
+    st = _strides4(x)
+    B, H, S, D = x.shape
+    q = torch.empty((B, H, S, D), dtype=torch.int8, device=x.device)
+    s = torch.empty(H, dtype=torch.float32, device=x.device)
+    own = status or StatusWord(x.device)
+    check(lib().reef_quantize_int8_per_head(_ptr(x), B, H, S, D, C.byref(st), _ptr(q), _ptr(s),
+                                            own.ptr, _stream()), "quantize_per_head")
+    if status is None:
+        own.check("quantize_per_head requires finite values")
+    return q, s
+
+
+def quantize_rows(x, status: StatusWord | None = None):
+    """quantize_rows (quant.hpp:112-133) over the last dimension: one scale per row
+    (per token). Returns int8 of x's shape and scales of x.shape[:-1]."""
+    torch = _torch()
+    _require(x, torch.float32, "x")
+    width = x.shape[-1]
+    x2 = x.reshape(-1, width)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    q = torch.empty((rows, width), dtype=torch.int8, device=x.device)
+    s = torch.empty(rows, dtype=torch.float32, device=x.device)
+    own = status or StatusWord(x.device)
+    check(lib().reef_quantize_int8_per_token(_ptr(x2), rows, width, x2.stride(0), _ptr(q),
+                                             _ptr(s), own.ptr, _stream()), "quantize_rows")
+    if status is None:
+        own.check("quantize_rows requires finite values")
+    return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+quantize_per_token = quantize_rows
+
+
+def dequantize(q, scales, group: int):
+    """x[i] = float(q[i]) * scales[i // group]."""
+    torch = _torch()
+    _require(q, torch.int8, "q")
+    _require(scales, torch.float32, "scales")
+    q = q.contiguous()
+    x = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    check(lib().reef_dequantize_int8(_ptr(q), q.numel(), group, _ptr(scales.contiguous()),
+                                     _ptr(x), _stream()), "dequantize")
+    return x
+
+
+# --- attention ------------------------------------------------------------------------
+
+def attention_prefill(q, k, v, q_scales, k_scales, v_scales, *, query_start=None, window=0,
+                      softmax_scale=None, q_granularity=PER_HEAD, kv_granularity=PER_HEAD,
+                      precise=False, out=None):
+    """Attention::context (attention.hpp:374-432) over int8 heads in one launch.
+
+    q [B, Hq, Sq, D], k and v [B, Hkv, Skv, D] int8 (contiguous head_dim, any other
+    strides); scales by granularity. softmax_scale defaults to 1/sqrt(D); pass 1.0
+    for the engine's unscaled scores. Returns fp32 [B, Hq, Sq, D].
+    """
+    torch = _torch()
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t, torch.int8, n)
+    for t, n in ((q_scales, "q_scales"), (k_scales, "k_scales"), (v_scales, "v_scales")):
+        _require(t, torch.float32, n)
+    B, Hq, Sq, D = q.shape
+    _, Hkv, Skv, _ = k.shape
+    if tuple(v.shape) != tuple(k.shape) or k.shape[0] != B or k.shape[3] != D:
+        raise InvalidArgument("attention_prefill shape mismatch")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    start = Skv - Sq if query_start is None else query_start
+    p = AttentionParams(B, Hq, Hkv, Sq, Skv, D, start, window, softmax_scale, q_granularity,
+                        kv_granularity, ATTN_PRECISE_PV if precise else 0)
+    if out is None:
+        out = torch.empty((B, Hq, Sq, D), dtype=torch.float32, device=q.device)
+    qs, ks, vs, os_ = _strides4(q), _strides4(k), _strides4(v), _strides4(out)
+    check(lib().reef_attention_prefill_int8(
+        C.byref(p), _ptr(q), C.byref(qs), _ptr(k), C.byref(ks), _ptr(v), C.byref(vs),
+        _ptr(q_scales.contiguous()), _ptr(k_scales.contiguous()), _ptr(v_scales.contiguous()),
+        _ptr(out), C.byref(os_), _stream()), "attention_prefill")
+    return out
+
+
+def qk_scores_i32(q, k):
+    """int32 q . k^T for packed q [B, Hq, Sq, D] and k [B, Hkv, Skv, D]."""
+    torch = _torch()
+    _require(q, torch.int8, "q")
+    _require(k, torch.int8, "k")
+    q = q.contiguous()
+    k = k.contiguous()
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    acc = torch.empty((B, Hq, Sq, Skv), dtype=torch.int32, device=q.device)
+    check(lib().reef_qk_scores_i32(_ptr(q), _ptr(k), B, Hq, Hkv, Sq, Skv, D, _ptr(acc),
+                                   _stream()), "qk_scores_i32")
+    return acc
+
+
+def _decode_params(q, max_context, kv_heads, window, softmax_scale, q_granularity, num_splits):
+    B, Hq, D = q.shape
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    return DecodeParams(B, Hq, kv_heads, D, max_context, window, softmax_scale, q_granularity,
+                        num_splits, 0)
+
+
+def decode_workspace(params: DecodeParams, device):
+    torch = _torch()
+    n = lib().reef_attention_decode_workspace_bytes(C.byref(params))
+    return torch.empty(max(n, 16) // 4 + 4, dtype=torch.float32, device=device)
+
+
+def attention_decode(q, q_scales, k_cache, v_pages, k_scales, v_scales, context_lens=None, *,
+                     window=0, softmax_scale=None, q_granularity=PER_TOKEN, num_splits=0,
+                     workspace=None, status: StatusWord | None = None, out=None):
+    """One decode step over a contiguous int8 cache.
+
+    q [B, Hq, D] int8; k_cache [B, Hkv, L, D]; v_pages [B, Hkv, L/16, D, 16] (see
+    pack_v_pages); k_scales, v_scales [B, Hkv, L]; context_lens [B] int32 or None.
+    """
+    torch = _torch()
+    _require(q, torch.int8, "q")
+    B, Hq, D = q.shape
+    Hkv, L = k_cache.shape[1], k_cache.shape[2]
+    if tuple(k_cache.shape) != (B, Hkv, L, D) or v_pages.numel() != k_cache.numel():
+        raise InvalidArgument("attention_decode cache shape mismatch")
+    p = _decode_params(q, L, Hkv, window, softmax_scale, q_granularity, num_splits)
+    ws = workspace if workspace is not None else decode_workspace(p, q.device)
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=q.device)
+    own = status or StatusWord(q.device)
+    cl = context_lens.contiguous() if context_lens is not None else None
+    check(lib().reef_attention_decode_int8(
+        C.byref(p), _ptr(q.contiguous()), _ptr(q_scales.contiguous()), _ptr(k_cache.contiguous()),
+        _ptr(v_pages.contiguous()), _ptr(k_scales.contiguous()), _ptr(v_scales.contiguous()),
+        _ptr(cl), _ptr(out), _ptr(ws), ws.numel() * 4, own.ptr, _stream()), "attention_decode")
+    if status is None:
+        own.check("attention_decode")
+    return out
+
+
+def attention_decode_paged(q, q_scales, k_pages, v_pages, k_scale_pages, v_scale_pages,
+                           block_table, context_lens, *, window=0, softmax_scale=None,
+                           q_granularity=PER_TOKEN, num_splits=0, workspace=None,
+                           status: StatusWord | None = None, out=None):
+    """One decode step over a paged int8 cache: k_pages [P, Hkv, 16, D], v_pages
+    [P, Hkv, D, 16], scale pages [P, Hkv, 16], block_table [B, max_blocks] int32,
+    context_lens [B] int32."""
+    torch = _torch()
+    _require(q, torch.int8, "q")
+    B, Hq, D = q.shape
+    P, Hkv = k_pages.shape[0], k_pages.shape[1]
+    max_blocks = block_table.shape[1]
+    p = _decode_params(q, max_blocks * PAGE, Hkv, window, softmax_scale, q_granularity,
+                       num_splits)
+    ws = workspace if workspace is not None else decode_workspace(p, q.device)
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=q.device)
+    own = status or StatusWord(q.device)
+    check(lib().reef_attention_decode_int8_paged(
+        C.byref(p), _ptr(q.contiguous()), _ptr(q_scales.contiguous()), _ptr(k_pages),
+        _ptr(v_pages), _ptr(k_scale_pages), _ptr(v_scale_pages), _ptr(block_table.contiguous()),
+        max_blocks, P, _ptr(context_lens.contiguous()), _ptr(out), _ptr(ws), ws.numel() * 4,
+        own.ptr, _stream()), "attention_decode_paged")
+    if status is None:
+        own.check("attention_decode_paged")
+    return out
+
+
+def pack_v_pages(v_tokens):
+    """Token-major values [..., pages * 16, D] -> transposed pages [..., pages, D, 16]."""
+    torch = _torch()
+    _require(v_tokens, torch.int8, "v_tokens")
+    *lead, L, D = v_tokens.shape
+    if L % PAGE:
+        raise InvalidArgument("token count must be a multiple of 16")
+    src = v_tokens.contiguous()
+    pages = src.numel() // (PAGE * D)
+    out = torch.empty((*lead, L // PAGE, D, PAGE), dtype=torch.int8, device=src.device)
+    check(lib().reef_kv_pack_v_pages(_ptr(src), pages, D, _ptr(out), _stream()), "pack_v_pages")
+    return out

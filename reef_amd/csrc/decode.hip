@@ -1,0 +1,441 @@
+// Decode attention over an int8 KV cache for gfx950: one query token per
+// sequence, all query heads of a KV head group served by one wave, the keys
+// split across waves (flash-decoding), partial (max, sum, output) combined by
+// a log-sum-exp pass.
+//
+// The engine's decode step is Attention::forward with query_len = 1
+// (attention.hpp:354-372): context() sees every cached key, query_start =
+// key_len - 1 (:415). Per (sequence, query head) this computes
+//   s_j = float(int32 q . k_j) * (s_q * s_k[j]) * softmax_scale,
+//   out = sum_j softmax(s)_j * float(v_j) * s_v[j].
+//
+// The kernel streams the cache straight from HBM into registers (no LDS): each
+// lane issues 16-byte loads that are exactly its matrix-instruction operands.
+//   * S^T = K . q^T on v_mfma_i32_16x16x64_i8: a 16-key x 16-head block per
+//     instruction; lane group g of the output holds keys 16g + 4t + i, i.e. the
+//     whole 16-token page g of the 64-key block.
+//   * out = P . V on v_mfma_f32_16x16x32_f16: P comes from the score registers
+//     unchanged (page g's 16 keys are lane group g's P operand), and V pages are
+//     stored transposed ([D, 16] per page), so a lane's V operand for one channel
+//     and 16 keys is one 16-byte load, converted exactly to fp16.
+// Only G = q_heads / kv_heads of the 16 instruction columns are live (4 for
+// 4:1 grouping); the instructions are far from the bound, HBM is.
+#include <algorithm>
+#include <cmath>
+
+#include "reef_common.hpp"
+
+namespace reef {
+namespace {
+
+constexpr int kDecodeWaves = 4;          // waves per workgroup, one split each
+constexpr int kBlockKeys = 64;           // keys per inner step (4 pages)
+constexpr int kPage = 16;                // tokens per page
+
+struct DecodeArgs {
+    const int8_t *q;
+    const float *qs;
+    const int8_t *k;        // contiguous cache or page pool
+    const int8_t *v;
+    const float *ks, *vs;
+    const int32_t *block_table;  // paged only
+    const int32_t *context_lens; // may be null
+    float *part_o;          // [B, Hq, splits, D]
+    float *part_ml;         // [B, Hq, splits, 2] (max in log2 units, sum)
+    uint32_t *status;
+    int32_t batch, q_heads, kv_heads, group;
+    int32_t max_context, window, splits, chunk;  // chunk: keys per split, multiple of 64
+    int32_t max_blocks, num_pages;               // paged only
+    int32_t q_gran;
+    float score_scale;  // softmax_scale * log2(e)
+};
+
+// Addresses of one 16-token page of (sequence b, kv head kvh). Pages at or past
+// n_pages (the sequence's ceil(len / 16)) are never looked up: they point at a
+// safe page and are dead. A page number outside [0, num_pages) is an error.
+struct PageRef {
+    const int8_t *k;   // [16, D]
+    const int8_t *vt;  // [D, 16]
+    const float *ks, *vs;  // [16]
+    bool live;  // holds keys of this sequence
+    bool ok;    // false: the block table held an out-of-range page number
+};
+
+template <int D, bool PAGED>
+__device__ __forceinline__ PageRef page_ref(const DecodeArgs &a, int b, int kvh, int page_idx,
+                                            int n_pages) {
+    PageRef r;
+    const bool in_seq = page_idx < n_pages;
+    if (PAGED) {
+        int page = in_seq ? a.block_table[(int64_t)b * a.max_blocks + page_idx] : 0;
+        const bool valid = page >= 0 && page < a.num_pages;
+        r.ok = valid || !in_seq;
+        r.live = in_seq && valid;
+        if (!valid) page = 0;
+        const int64_t slot = (int64_t)page * a.kv_heads + kvh;
+        r.k = a.k + slot * (kPage * D);
+        r.vt = a.v + slot * (kPage * D);
+        r.ks = a.ks + slot * kPage;
+        r.vs = a.vs + slot * kPage;
+    } else {
+        r.ok = true;
+        r.live = in_seq;
+        const int64_t seq = (int64_t)b * a.kv_heads + kvh;
+        const int64_t tok = seq * a.max_context + (int64_t)(in_seq ? page_idx : 0) * kPage;
+        r.k = a.k + tok * D;
+        r.vt = a.v + tok * D;  // pages of [D, 16] are contiguous in the same order
+        r.ks = a.ks + tok;
+        r.vs = a.vs + tok;
+    }
+    return r;
+}
+
+// int8 x 16 (one 16-byte word) -> two fp16 x 8 operands, exactly.
+__device__ __forceinline__ void int8x16_to_f16(i32x4 w, f16x8 &lo, f16x8 &hi) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        lo[e] = (_Float16)(int)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+        hi[e] = (_Float16)(int)(int8_t)(w[2 + (e >> 2)] >> (8 * (e & 3)));
+    }
+}
+
+template <int D, bool PAGED>
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a) {
+    constexpr int KS = D / 64;   // 64-wide reduction steps of the score instruction
+    constexpr int DB = D / 16;   // 16-wide output blocks
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int split = blockIdx.x * kDecodeWaves + wave;
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    if (split >= a.splits) return;
+
+    const int head = kvh * a.group + col;   // this lane's query head (live if col < group)
+    const bool head_ok = col < a.group;
+
+    int len = a.context_lens ? a.context_lens[b] : a.max_context;
+    if (len < 1 || len > a.max_context) {
+        if (split == 0 && lane == 0) flag_status(a.status, REEF_STATUS_BIT_BAD_LENGTH);
+        len = 0;
+    }
+    const int lo = a.window > 0 ? max(0, len - a.window) : 0;
+    const int k_begin = max(split * a.chunk, lo / kBlockKeys * kBlockKeys);
+    const int k_end = min((split + 1) * a.chunk, len);
+    const int n_pages = (len + kPage - 1) / kPage;
+
+    // q^T operand: 16 bytes of head `head` per 64-wide reduction step.
+    i32x4 qop[KS];
+    const int8_t *qrow = a.q + ((int64_t)b * a.q_heads + (head_ok ? head : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+        qop[s] = head_ok ? *reinterpret_cast<const i32x4 *>(qrow + 64 * s + 16 * grp)
+                         : i32x4{0, 0, 0, 0};
+    float cq = 0.0f;
+    if (head_ok) {
+        cq = a.q_gran == REEF_SCALE_PER_TENSOR ? a.qs[0]
+             : a.q_gran == REEF_SCALE_PER_HEAD ? a.qs[head]
+                                                : a.qs[(int64_t)b * a.q_heads + head];
+    }
+    const float c = cq * a.score_scale;
+
+    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f;
+    f32x4 acc[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) acc[d] = f32x4{};
+    bool bad_page = false;
+
+    for (int kb = k_begin; kb < k_end; kb += kBlockKeys) {
+        const int page0 = kb / kPage;
+        // K rows for the score instruction: row m = col of block t is key
+        // 16 (m / 4) + 4t + (m % 4), in page m / 4.
+        const PageRef kp = page_ref<D, PAGED>(a, b, kvh, page0 + (col >> 2), n_pages);
+        // This lane group's page for scales, P and V.
+        const PageRef gp = page_ref<D, PAGED>(a, b, kvh, page0 + grp, n_pages);
+        bad_page |= !gp.ok;
+
+        i32x4 kop[4][KS];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+                kop[t][s] = *reinterpret_cast<const i32x4 *>(kp.k + (4 * t + (col & 3)) * D +
+                                                             64 * s + 16 * grp);
+        i32x4 vop[DB];
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+            vop[d] = *reinterpret_cast<const i32x4 *>(gp.vt + (16 * d + col) * kPage);
+        f32x4 ksc[4], vsc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            ksc[t] = *reinterpret_cast<const f32x4 *>(gp.ks + 4 * t);
+            vsc[t] = *reinterpret_cast<const f32x4 *>(gp.vs + 4 * t);
+        }
+
+        float x[16];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            i32x4 s = {0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) s = mfma_16x16x64_i8(kop[t][ks], qop[ks], s);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[4 * t + i] = (float)s[i] * (c * ksc[t][i]);
+        }
+        // Keys outside [lo, k_end) or on a dead page take no part: score -inf and
+        // value scale 0 (the cache past a sequence's end may hold anything).
+        float vv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kb + 16 * grp + r;
+            const bool vis = key >= lo && key < k_end && gp.live;
+            if (!vis) x[r] = -INFINITY;
+            vv[r] = vis ? vsc[r >> 2][r & 3] : 0.0f;
+        }
+        float mt = x[0], vmax = vv[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) {
+            mt = fmaxf(mt, x[r]);
+            vmax = fmaxf(vmax, vv[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        // Values accumulate in units of s_run, the largest value scale so far,
+        // so p * v_scale / s_run stays within [0, 1] in fp16.
+        const float s_new = fmaxf(s_run, vmax);
+        const float alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
+        const float inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
+        m_run = m_new;
+        s_run = s_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
+
+        // P operand: lane group g's keys 16g + 8h + e for the two halves h.
+        f16x8 pop[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = __builtin_amdgcn_exp2f(x[r] - m_use);
+            l_run += p;
+            pop[r >> 3][r & 7] = (_Float16)(p * (vv[r] * inv_s));
+        }
+        // The 16x16 instruction's rows are heads, so the P operand is laid out
+        // with the head in lane % 16 -- which is where the score output put it.
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            f16x8 v0, v1;
+            int8x16_to_f16(vop[d], v0, v1);
+            acc[d] = mfma_16x16x32_f16(pop[0], v0, acc[d]);
+            acc[d] = mfma_16x16x32_f16(pop[1], v1, acc[d]);
+        }
+    }
+    if (bad_page) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
+
+    // Row sums: this lane holds head col's partial over its 16 keys per block.
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    // acc[d][i] is (head 4 grp + i, channel 16 d + col); write live heads.
+    const int64_t base_bh = (int64_t)b * a.q_heads + kvh * a.group;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * grp + i;
+        if (hh >= a.group) continue;
+        float *po = a.part_o + ((base_bh + hh) * a.splits + split) * D;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) po[16 * d + col] = acc[d][i] * s_run;
+    }
+    if (head_ok && grp == 0) {
+        float *ml = a.part_ml + ((base_bh + col) * a.splits + split) * 2;
+        ml[0] = m_run;
+        ml[1] = l_run;
+    }
+}
+
+// out[b, h, :] = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s.
+template <int D>
+__global__ __launch_bounds__(64) void decode_combine(const float *__restrict__ part_o,
+                                                     const float *__restrict__ part_ml,
+                                                     int32_t splits, float *__restrict__ out) {
+    const int64_t bh = blockIdx.x;
+    const int lane = threadIdx.x;
+    const float *ml = part_ml + bh * splits * 2;
+    float m = -INFINITY;
+    for (int s = 0; s < splits; ++s) m = fmaxf(m, ml[2 * s]);
+    const float m_use = m == -INFINITY ? 0.0f : m;
+    float l = 0.0f;
+    float o[D / 64];
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) o[j] = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+        const float w = __builtin_amdgcn_exp2f(ml[2 * s] - m_use);
+        l += ml[2 * s + 1] * w;
+        const float *po = part_o + (bh * splits + s) * D;
+#pragma unroll
+        for (int j = 0; j < D / 64; ++j) o[j] += po[64 * j + lane] * w;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) out[bh * D + 64 * j + lane] = o[j] * inv;
+}
+
+__global__ void pack_v_pages(const int8_t *__restrict__ v_tokens, int64_t pages, int32_t dim,
+                             int8_t *__restrict__ v_pages) {
+    // One thread per (page, channel): gathers 16 bytes with stride dim.
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= pages * dim) return;
+    const int64_t page = i / dim;
+    const int d = (int)(i % dim);
+    const int8_t *src = v_tokens + page * kPage * dim + d;
+    int8_t buf[kPage];
+#pragma unroll
+    for (int t = 0; t < kPage; ++t) buf[t] = src[(int64_t)t * dim];
+    *reinterpret_cast<i32x4 *>(v_pages + (page * dim + d) * kPage) =
+        *reinterpret_cast<const i32x4 *>(buf);
+}
+
+int default_splits(const reef_decode_params *p) {
+    if (p->num_splits > 0) return p->num_splits;
+    const int64_t blocks = ceil_div(p->max_context, kBlockKeys);
+    const int64_t pairs = p->batch * p->kv_heads;
+    // Aim for about 4096 waves over the 256 compute units, at least 4 blocks
+    // (256 keys) per split.
+    int64_t s = ceil_div(4096, pairs);
+    s = std::min<int64_t>(s, ceil_div(blocks, 4));
+    return (int)std::max<int64_t>(1, s);
+}
+
+reef_status validate(const reef_decode_params *p, const int8_t *q, const float *q_scales,
+                     float *out, void *workspace, size_t workspace_bytes) {
+    if (!p || !q || !q_scales || !out || !workspace) return REEF_INVALID_ARGUMENT;
+    if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->max_context <= 0 ||
+        p->q_heads % p->kv_heads != 0 || p->window < 0 || p->num_splits < 0 ||
+        p->max_context % kPage != 0 || !std::isfinite(p->softmax_scale) ||
+        (p->q_granularity != REEF_SCALE_PER_TENSOR && p->q_granularity != REEF_SCALE_PER_HEAD &&
+         p->q_granularity != REEF_SCALE_PER_TOKEN))
+        return REEF_INVALID_ARGUMENT;
+    if (p->head_dim != 64 && p->head_dim != 128) return REEF_UNSUPPORTED;
+    if (p->q_heads / p->kv_heads > 16 || p->kv_heads > 65535 || p->batch > 65535 ||
+        p->max_context >= (int64_t(1) << 30))
+        return REEF_UNSUPPORTED;
+    if (!aligned(q, 16) || !aligned(out, 4) || !aligned(workspace, 16)) return REEF_INVALID_ARGUMENT;
+    if (workspace_bytes < reef_attention_decode_workspace_bytes(p)) return REEF_INVALID_ARGUMENT;
+    return REEF_OK;
+}
+
+template <bool PAGED>
+reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out,
+                          hipStream_t stream) {
+    const int splits = default_splits(p);
+    a.splits = splits;
+    a.chunk = (int32_t)(ceil_div(ceil_div(p->max_context, splits), kBlockKeys) * kBlockKeys);
+    a.batch = (int32_t)p->batch;
+    a.q_heads = (int32_t)p->q_heads;
+    a.kv_heads = (int32_t)p->kv_heads;
+    a.group = (int32_t)(p->q_heads / p->kv_heads);
+    a.max_context = (int32_t)p->max_context;
+    a.window = (int32_t)std::min<int64_t>(p->window, INT32_MAX);
+    a.q_gran = p->q_granularity;
+    a.score_scale = p->softmax_scale * kLog2e;
+    const dim3 grid((unsigned)ceil_div(splits, kDecodeWaves), (unsigned)p->kv_heads,
+                    (unsigned)p->batch);
+    if (p->head_dim == 128)
+        hipLaunchKernelGGL((decode_kernel<128, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<64, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
+    const dim3 cgrid((unsigned)(p->batch * p->q_heads));
+    if (p->head_dim == 128)
+        hipLaunchKernelGGL(decode_combine<128>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml,
+                           splits, out);
+    else
+        hipLaunchKernelGGL(decode_combine<64>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml,
+                           splits, out);
+    return launch_status();
+}
+
+void set_workspace(DecodeArgs &a, const reef_decode_params *p, void *workspace) {
+    const int64_t rows = p->batch * p->q_heads * (int64_t)default_splits(p);
+    a.part_o = static_cast<float *>(workspace);
+    a.part_ml = a.part_o + rows * p->head_dim;
+}
+
+}  // namespace
+}  // namespace reef
+
+using namespace reef;
+
+extern "C" size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p) {
+    if (!p || p->batch <= 0 || p->q_heads <= 0 || p->head_dim <= 0 || p->max_context <= 0)
+        return 0;
+    const int64_t rows = p->batch * p->q_heads * (int64_t)default_splits(p);
+    return (size_t)(rows * (p->head_dim + 2) * sizeof(float));
+}
+
+extern "C" reef_status reef_attention_decode_int8(const reef_decode_params *p, const int8_t *q,
+                                                  const float *q_scales, const int8_t *k_cache,
+                                                  const int8_t *v_cache, const float *k_scales,
+                                                  const float *v_scales,
+                                                  const int32_t *context_lens, float *out,
+                                                  void *workspace, size_t workspace_bytes,
+                                                  uint32_t *status_word, hipStream_t stream) {
+    reef_status st = validate(p, q, q_scales, out, workspace, workspace_bytes);
+    if (st != REEF_OK) return st;
+    if (!k_cache || !v_cache || !k_scales || !v_scales || !aligned(k_cache, 16) ||
+        !aligned(v_cache, 16) || !aligned(k_scales, 16) || !aligned(v_scales, 16))
+        return REEF_INVALID_ARGUMENT;
+    DecodeArgs a = {};
+    a.q = q;
+    a.qs = q_scales;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.ks = k_scales;
+    a.vs = v_scales;
+    a.context_lens = context_lens;
+    a.status = status_word;
+    set_workspace(a, p, workspace);
+    return launch_decode<false>(p, a, out, stream);
+}
+
+extern "C" reef_status reef_attention_decode_int8_paged(
+    const reef_decode_params *p, const int8_t *q, const float *q_scales, const int8_t *k_pages,
+    const int8_t *v_pages, const float *k_scale_pages, const float *v_scale_pages,
+    const int32_t *block_table, int64_t max_blocks_per_seq, int64_t num_pages,
+    const int32_t *context_lens, float *out, void *workspace, size_t workspace_bytes,
+    uint32_t *status_word, hipStream_t stream) {
+    reef_status st = validate(p, q, q_scales, out, workspace, workspace_bytes);
+    if (st != REEF_OK) return st;
+    if (!k_pages || !v_pages || !k_scale_pages || !v_scale_pages || !block_table ||
+        !context_lens || num_pages <= 0 || num_pages >= (int64_t(1) << 31) ||
+        max_blocks_per_seq * kPage < p->max_context || max_blocks_per_seq >= (int64_t(1) << 30) ||
+        !aligned(k_pages, 16) || !aligned(v_pages, 16) || !aligned(k_scale_pages, 16) ||
+        !aligned(v_scale_pages, 16))
+        return REEF_INVALID_ARGUMENT;
+    DecodeArgs a = {};
+    a.q = q;
+    a.qs = q_scales;
+    a.k = k_pages;
+    a.v = v_pages;
+    a.ks = k_scale_pages;
+    a.vs = v_scale_pages;
+    a.block_table = block_table;
+    a.context_lens = context_lens;
+    a.status = status_word;
+    a.max_blocks = (int32_t)max_blocks_per_seq;
+    a.num_pages = (int32_t)num_pages;
+    set_workspace(a, p, workspace);
+    return launch_decode<true>(p, a, out, stream);
+}
+
+extern "C" reef_status reef_kv_pack_v_pages(const int8_t *v_tokens, int64_t pages,
+                                            int64_t head_dim, int8_t *v_pages,
+                                            hipStream_t stream) {
+    if (!v_tokens || !v_pages || pages <= 0 || head_dim <= 0 || head_dim > 65536 ||
+        !aligned(v_pages, 16))
+        return REEF_INVALID_ARGUMENT;
+    const int64_t n = pages * head_dim;
+    hipLaunchKernelGGL(pack_v_pages, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream,
+                       v_tokens, pages, (int32_t)head_dim, v_pages);
+    return launch_status();
+}

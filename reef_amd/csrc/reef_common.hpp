@@ -1,0 +1,95 @@
+// Shared device and host helpers for the reef_hip kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "reef_hip/attention.h"
+
+namespace reef {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.44269504088896341f;
+
+// --- matrix instructions ---------------------------------------------------------------
+// Output layout of the 32x32 instructions: lane l holds column l % 32 and, in
+// register 4j + i, row 8j + 4(l / 32) + i. Of the 16x16 instructions: lane l
+// holds column l % 16 and, in register i, row 4(l / 16) + i. In both operands,
+// lane group l / 32 (l / 16) supplies the same slice of the reduction index, so
+// any consistent assignment of reduction indices to (group, element) is valid.
+
+__device__ __forceinline__ i32x16 mfma_32x32x32_i8(i32x4 a, i32x4 b, i32x16 c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x4 mfma_16x16x64_i8(i32x4 a, i32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x16_f16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x32_f16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// --- small device helpers -----------------------------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t w = (uint32_t)__shfl_xor((int)v, o);
+        v = v > w ? v : w;
+    }
+    return v;
+}
+
+// Scale of quant.hpp:51-57 from a largest magnitude: max / 127 (IEEE
+// division), or 1 when every value was zero.
+__device__ __forceinline__ float int8_scale(float max_magnitude) {
+    return max_magnitude > 0.0f ? max_magnitude / 127.0f : 1.0f;
+}
+
+// quantize_int8 of quant.hpp:68-81 for a finite value: nearbyint(x / scale),
+// ties to even (v_rndne_f32), clamped to +-127.
+__device__ __forceinline__ int8_t quantize_int8(float x, float scale) {
+    float r = __builtin_rintf(x / scale);
+    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+    return (int8_t)(int)r;
+}
+
+__device__ __forceinline__ void flag_status(uint32_t *word, uint32_t bits) {
+    if (word) atomicOr(word, bits);
+}
+
+// --- host helpers -----------------------------------------------------------------------
+
+inline bool aligned(const void *p, size_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+inline reef_status launch_status() {
+    return hipGetLastError() == hipSuccess ? REEF_OK : REEF_HIP_ERROR;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace reef

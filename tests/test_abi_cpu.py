@@ -1,0 +1,99 @@
+"""The C ABI without a GPU: the library loads, exports every entry point the
+public header declares, and rejects bad arguments on the host before any launch
+(the engine's error paths: attention.hpp:293-327, activation.hpp:204-207)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import reef_amd
+from reef_amd import AttentionParams, DecodeParams, Strides
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "reef_hip", "attention.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:reef_status|size_t)\s+(reef_[a-z0-9_]+)\s*\(", text,
+                                 re.M)))
+
+
+def test_library_exports_every_declared_entry_point():
+    names = declared()
+    assert len(names) >= 11
+    lib = reef_amd.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(reef_amd.EXPORTS) == names
+
+
+def _fake(n=1):
+    # Non-null, 256-byte aligned host addresses: validation never dereferences them.
+    return C.c_void_p(0x10000 * n)
+
+
+def _prefill(p, strides=None):
+    lib = reef_amd.lib()
+    s = C.byref(strides) if strides else None
+    return lib.reef_attention_prefill_int8(C.byref(p), _fake(1), s, _fake(2), s, _fake(3), s,
+                                           _fake(4), _fake(5), _fake(6), _fake(7), None, None)
+
+
+def good_params(**kw):
+    d = dict(batch=1, q_heads=4, kv_heads=2, q_len=8, kv_len=8, head_dim=128, query_start=0,
+             window=0, softmax_scale=0.1, q_granularity=1, kv_granularity=1, flags=0)
+    d.update(kw)
+    return AttentionParams(**d)
+
+
+@pytest.mark.parametrize("change,status", [
+    (dict(q_heads=3), reef_amd.INVALID_ARGUMENT),          # not a multiple of kv_heads
+    (dict(query_start=1), reef_amd.INVALID_ARGUMENT),      # rows past the last key
+    (dict(q_len=0), reef_amd.INVALID_ARGUMENT),
+    (dict(window=-1), reef_amd.INVALID_ARGUMENT),
+    (dict(q_granularity=7), reef_amd.INVALID_ARGUMENT),
+    (dict(softmax_scale=float("nan")), reef_amd.INVALID_ARGUMENT),
+    (dict(head_dim=96), reef_amd.UNSUPPORTED),
+    (dict(kv_len=1 << 31, q_len=8), reef_amd.UNSUPPORTED),
+])
+def test_prefill_host_validation(change, status):
+    assert _prefill(good_params(**change)) == status
+
+
+def test_prefill_rejects_null_and_misaligned():
+    lib = reef_amd.lib()
+    p = good_params()
+    assert lib.reef_attention_prefill_int8(C.byref(p), None, None, None, None, None, None, None,
+                                           None, None, None, None, None) == 1
+    assert _prefill(p, Strides(0, 128, 129)) == reef_amd.INVALID_ARGUMENT  # row not 16-B aligned
+
+
+def test_decode_host_validation_and_workspace():
+    lib = reef_amd.lib()
+    p = DecodeParams(batch=64, q_heads=32, kv_heads=8, head_dim=128, max_context=4096,
+                     window=0, softmax_scale=0.1, q_granularity=2, num_splits=0, flags=0)
+    ws = lib.reef_attention_decode_workspace_bytes(C.byref(p))
+    assert ws > 0 and ws % (64 * 32 * 130 * 4) == 0
+    f = [_fake(i) for i in range(1, 12)]
+    args = lambda pp, w: (C.byref(pp), f[0], f[1], f[2], f[3], f[4], f[5], None, f[6], f[7],  # noqa: E731
+                          w, None, None)
+    assert lib.reef_attention_decode_int8(*args(p, ws - 4)) == reef_amd.INVALID_ARGUMENT
+    bad = DecodeParams(64, 32, 8, 128, 4100, 0, 0.1, 2, 0, 0)  # not a multiple of 16
+    assert lib.reef_attention_decode_int8(*args(bad, 1 << 30)) == reef_amd.INVALID_ARGUMENT
+    wide = DecodeParams(1, 32, 1, 128, 64, 0, 0.1, 2, 0, 0)  # 32 heads per kv head
+    assert lib.reef_attention_decode_int8(*args(wide, 1 << 30)) == reef_amd.UNSUPPORTED
+    # paged: the block table must cover max_context
+    assert lib.reef_attention_decode_int8_paged(
+        C.byref(p), f[0], f[1], f[2], f[3], f[4], f[5], f[6], 4096 // 16 - 1, 100, f[7], f[8],
+        f[9], 1 << 30, None, None) == reef_amd.INVALID_ARGUMENT
+
+
+def test_quantize_host_validation():
+    lib = reef_amd.lib()
+    assert lib.reef_quantize_int8_per_tensor(_fake(), 0, _fake(), _fake(), None, None) == 1
+    assert lib.reef_quantize_int8_per_token(_fake(), 4, 8, 7, _fake(), _fake(), None, None) == 1
+    assert lib.reef_quantize_int8_per_head(None, 1, 1, 1, 1, None, _fake(), _fake(), None,
+                                           None) == 1
+    assert lib.reef_read_status_word(None, 0, None) == 1

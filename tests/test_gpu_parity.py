@@ -1,0 +1,333 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Integer outputs (int32 scores, int8 codes, scales) must be bit-exact; fp32
+attention outputs must be within max-abs-error 1e-3 of the oracle's golden
+(TOL below) on N(0, 1) data. Each case prints its name before touching the GPU.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from reef_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def reef():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import reef_amd
+    reef_amd.lib()  # raises if the library was not built
+    return reef_amd
+
+
+def case(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+def gpu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rand_i8(rng, shape, low=-127):
+    return rng.integers(low, 128, shape, dtype=np.int8)
+
+
+# --- bit-exact integer scores ----------------------------------------------------------
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D", [
+    (1, 1, 1, 128, 128, 64), (2, 4, 2, 37, 101, 128), (1, 2, 1, 1, 33, 64),
+    (1, 8, 1, 200, 96, 128), (3, 3, 3, 65, 17, 128)])
+def test_qk_scores_bit_exact(reef, B, Hq, Hkv, Sq, Skv, D):
+    case(f"qk_scores_i32 B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D}")
+    rng = np.random.default_rng(B * 1000 + Sq)
+    q = rand_i8(rng, (B, Hq, Sq, D), low=-128)
+    k = rand_i8(rng, (B, Hkv, Skv, D), low=-128)
+    k[0, 0, 0] = -128
+    q[0, 0, 0] = -128
+    acc = host(reef.qk_scores_i32(gpu(q), gpu(k)))
+    g = Hq // Hkv
+    want = np.einsum("bhqd,bhkd->bhqk", q.astype(np.int64),
+                     np.repeat(k, g, axis=1).astype(np.int64))
+    assert np.array_equal(acc, want)
+    assert acc[0, 0, 0, 0] == 128 * 128 * D
+    assert np.array_equal(acc[0, 0], oracle.qk_i32(q[0, 0], k[0, 0]))
+
+
+# --- bit-exact quantization ---------------------------------------------------------------
+
+def _ties(n):
+    """Values whose scale is exactly 1 (largest magnitude 127) so x / scale is x:
+    halves exercise ties-to-even in both signs."""
+    x = np.linspace(-126.5, 126.5, n).astype(np.float32)
+    x[: min(n, 9)] = np.array([127, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 126.5, -1.5], np.float32)[: min(n, 9)]
+    return x
+
+
+def test_quantize_per_tensor_bit_exact(reef):
+    case("quantize_per_tensor n=1000003 normal + ties")
+    x = (W.lcg_normal(21, 1_000_003) * 3.7).astype(np.float32)
+    q, s = reef.quantize_per_tensor(gpu(x))
+    qo, so = oracle.quantize_per_tensor(x)
+    assert host(s)[0].view(np.uint32) == so[0].view(np.uint32)
+    assert np.array_equal(host(q), qo)
+    t = _ties(1001)
+    q, s = reef.quantize_per_tensor(gpu(t))
+    qo, so = oracle.quantize_per_tensor(t)
+    assert host(s)[0] == 1.0 and np.array_equal(host(q), qo)
+    z = np.zeros(17, np.float32)
+    q, s = reef.quantize_per_tensor(gpu(z))
+    assert host(s)[0] == 1.0 and not host(q).any()  # an all-zero tensor keeps scale 1
+
+
+def test_quantize_per_head_bit_exact_with_strides(reef):
+    case("quantize_per_head [2, 6, 33, 128] from a [B, S, H, D] layout")
+    x = W.lcg_normal(22, 2 * 33 * 6 * 128).reshape(2, 33, 6, 128)
+    x[:, :, 3] *= 50.0
+    x[:, :, 5] = 0.0
+    xt = gpu(x).permute(0, 2, 1, 3)  # [B, H, S, D] view with strides
+    q, s = reef.quantize_per_head(xt)
+    qo, so = oracle.quantize_per_head(np.ascontiguousarray(x.transpose(0, 2, 1, 3)))
+    assert np.array_equal(host(s).view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(host(q), qo)
+    assert host(s)[5] == 1.0
+
+
+@pytest.mark.parametrize("rows,width", [(4096, 128), (7, 37), (300, 64), (3, 1)])
+def test_quantize_rows_bit_exact(reef, rows, width):
+    case(f"quantize_rows {rows}x{width}")
+    x = W.lcg_normal(23 + width, rows * width).reshape(rows, width)
+    x *= W.lcg_uniform(24, rows, 0.01, 40.0)[:, None]
+    if rows > 3:
+        x[1] = 0.0
+        x[2, : min(width, 9)] = _ties(min(width, 9))
+    q, s = reef.quantize_rows(gpu(x))
+    qo, so = oracle.quantize_rows(x)
+    assert np.array_equal(host(s).view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(host(q), qo)
+
+
+def test_quantize_rows_with_row_stride(reef):
+    case("quantize_rows over a strided [rows, 128] view")
+    x = W.lcg_normal(25, 64 * 256).reshape(64, 256)
+    view = gpu(x)[:, 64:192]
+    q, s = reef.quantize_rows(view)
+    qo, so = oracle.quantize_rows(np.ascontiguousarray(x[:, 64:192]))
+    assert np.array_equal(host(q), qo) and np.array_equal(host(s), so)
+
+
+def test_quantize_rejects_non_finite(reef):
+    case("quantize non-finite -> NonFiniteInput")
+    for bad in (math.nan, math.inf, -math.inf):
+        x = np.ones((4, 64), np.float32)
+        x[2, 5] = bad
+        with pytest.raises(reef.NonFiniteInput):
+            reef.quantize_rows(gpu(x))
+        with pytest.raises(reef.NonFiniteInput):
+            reef.quantize_per_tensor(gpu(x))
+        with pytest.raises(reef.NonFiniteInput):
+            reef.quantize_per_head(gpu(x.reshape(1, 2, 2, 64)))
+    reef.quantize_rows(gpu(np.ones((4, 64), np.float32)))  # the status word is clean again
+
+
+# --- prefill attention ----------------------------------------------------------------------
+
+def _quantize(x, gran):
+    if gran == oracle.GRAN_TENSOR:
+        return oracle.quantize_per_tensor(x)
+    if gran == oracle.GRAN_HEAD:
+        return oracle.quantize_per_head(x)
+    return oracle.quantize_per_token(x)
+
+
+def _run_prefill(reef, q, k, v, p, precise=False):
+    qq, qs = _quantize(q, p.q_granularity)
+    kq, ks = _quantize(k, p.kv_granularity)
+    vq, vs = _quantize(v, p.kv_granularity)
+    out = reef.attention_prefill(gpu(qq), gpu(kq), gpu(vq), gpu(qs), gpu(ks), gpu(vs),
+                                 query_start=p.start(), window=p.window,
+                                 softmax_scale=p.softmax_scale, q_granularity=p.q_granularity,
+                                 kv_granularity=p.kv_granularity, precise=precise)
+    gold = oracle.attention_int8(p, qq, kq, vq, qs, ks, vs)
+    return host(out), gold
+
+
+def test_prefill_config1(reef):
+    cfg = W.CONFIGS["c1"]
+    case(f"prefill {cfg.name}")
+    q, k, v = W.host_prefill_inputs(cfg)
+    # the kernels' quantization is bit-identical to the oracle's
+    qg, sg = reef.quantize_per_tensor(gpu(q))
+    qo, so = oracle.quantize_per_tensor(q)
+    assert np.array_equal(host(qg), qo) and host(sg)[0] == so[0]
+    p = oracle.Problem(1, 1, 1, 128, 128, 64, softmax_scale=cfg.softmax_scale,
+                       q_granularity=0, kv_granularity=0)
+    out, gold = _run_prefill(reef, q, k, v, p)
+    err = np.abs(out - gold).max()
+    print(f"max_abs_err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+PREFILL_CASES = [
+    # B, Hq, Hkv, Sq, Skv, D, query_start, window, q_gran, kv_gran, softmax_scale
+    (1, 2, 2, 256, 256, 128, None, 0, 1, 1, None),
+    (2, 4, 1, 200, 200, 128, None, 0, 1, 1, None),       # GQA 4:1, ragged q tile
+    (1, 8, 1, 130, 333, 128, None, 0, 1, 1, None),       # decode-like offset: query_start 203
+    (1, 2, 2, 300, 300, 64, None, 40, 0, 0, None),       # sliding window 40
+    (1, 2, 1, 96, 500, 128, 100, 70, 2, 2, None),        # explicit start, window, per-token
+    (2, 2, 2, 77, 77, 128, None, 0, 2, 1, 1.0),          # engine's unscaled scores
+    (1, 1, 1, 1, 1, 64, None, 0, 1, 1, None),            # a single token
+    (1, 4, 4, 513, 513, 128, None, 0, 1, 2, None),       # per-token K/V scales
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D,start,window,gq,gkv,scale", PREFILL_CASES)
+def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq, gkv, scale):
+    case(f"prefill B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} start{start} win{window} "
+         f"gq{gq} gkv{gkv} scale{scale}")
+    seed = B * 7 + Sq * 3 + Skv + D + window
+    q = W.lcg_normal(seed, B * Hq * Sq * D).reshape(B, Hq, Sq, D)
+    k = W.lcg_normal(seed + 1, B * Hkv * Skv * D).reshape(B, Hkv, Skv, D)
+    v = W.lcg_normal(seed + 2, B * Hkv * Skv * D).reshape(B, Hkv, Skv, D)
+    if scale == 1.0:  # keep unscaled scores moderate
+        q *= 0.1
+        k *= 0.1
+    p = oracle.Problem(B, Hq, Hkv, Sq, Skv, D, query_start=start, window=window,
+                       softmax_scale=(1 / math.sqrt(D)) if scale is None else scale,
+                       q_granularity=gq, kv_granularity=gkv)
+    for precise in (False, True):
+        out, gold = _run_prefill(reef, q, k, v, p, precise)
+        err = np.abs(out - gold).max()
+        print(f"precise={precise} max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL, (precise, err)
+
+
+def test_prefill_rejects_bad_arguments(reef):
+    case("prefill argument errors")
+    z = torch.zeros((1, 1, 8, 128), dtype=torch.int8, device="cuda")
+    s = torch.ones(1, dtype=torch.float32, device="cuda")
+    with pytest.raises(reef.InvalidArgument):  # query rows past the keys
+        reef.attention_prefill(z, z, z, s, s, s, query_start=4)
+    with pytest.raises(reef.Unsupported):
+        zz = torch.zeros((1, 1, 8, 96), dtype=torch.int8, device="cuda")
+        reef.attention_prefill(zz, zz, zz, s, s, s)
+
+
+# --- decode ----------------------------------------------------------------------------------
+
+def _decode_problem(B, Hq, Hkv, D, lens, seed, max_ctx):
+    """fp32 draws quantized per token, as the cache stores them."""
+    q = W.lcg_normal(seed, B * Hq * D).reshape(B, Hq, D)
+    kf = W.lcg_normal(seed + 1, B * Hkv * max_ctx * D).reshape(B, Hkv, max_ctx, D)
+    vf = W.lcg_normal(seed + 2, B * Hkv * max_ctx * D).reshape(B, Hkv, max_ctx, D)
+    qq, qs = oracle.quantize_rows(q.reshape(B * Hq, D))
+    kq, ks = oracle.quantize_per_token(kf)
+    vq, vs = oracle.quantize_per_token(vf)
+    return qq.reshape(B, Hq, D), qs.reshape(B, Hq), kq, ks, vq, vs
+
+
+def _decode_gold(qq, qs, kq, ks, vq, vs, lens, window, scale):
+    B, Hq, D = qq.shape
+    Hkv = kq.shape[1]
+    out = np.zeros((B, Hq, D), np.float32)
+    for b in range(B):
+        L = int(lens[b])
+        p = oracle.Problem(1, Hq, Hkv, 1, L, D, window=window, softmax_scale=scale,
+                           q_granularity=2, kv_granularity=2)
+        out[b] = oracle.attention_int8(p, qq[b:b + 1, :, None], kq[b:b + 1, :, :L],
+                                       vq[b:b + 1, :, :L], qs[b], ks[b, :, :L], vs[b, :, :L])[0, :, 0]
+    return out
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,lens,window,splits", [
+    (3, 8, 2, 128, [256, 100, 17], 0, 0),
+    (2, 32, 8, 128, [1024, 1024], 0, 0),
+    (4, 4, 4, 64, [64, 1, 300, 129], 0, 3),
+    (2, 16, 1, 128, [700, 333], 50, 0),
+])
+def test_decode_contiguous_matches_oracle(reef, B, Hq, Hkv, D, lens, window, splits):
+    max_ctx = ((max(lens) + 15) // 16) * 16
+    case(f"decode contiguous B{B} Hq{Hq} Hkv{Hkv} D{D} lens{lens} win{window} splits{splits}")
+    qq, qs, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 31 + B + D, max_ctx)
+    scale = 1 / math.sqrt(D)
+    v_pages = reef.pack_v_pages(gpu(vq))
+    assert np.array_equal(host(v_pages),
+                          vq.reshape(B, Hkv, max_ctx // 16, 16, D).transpose(0, 1, 2, 4, 3))
+    out = reef.attention_decode(gpu(qq), gpu(qs), gpu(kq), v_pages, gpu(ks), gpu(vs),
+                                gpu(np.array(lens, np.int32)), window=window,
+                                softmax_scale=scale, num_splits=splits)
+    gold = _decode_gold(qq, qs, kq, ks, vq, vs, lens, window, scale)
+    err = np.abs(host(out) - gold).max()
+    print(f"max_abs_err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def _paged(kq, ks, vq, vs, lens, seed, slack=1.5):
+    """Scatter each sequence's pages into a pool at seeded positions."""
+    B, Hkv, Lmax, D = kq.shape
+    npages = [(int(L) + 15) // 16 for L in lens]
+    pool = int(sum(npages) * slack) + 1
+    order = np.argsort(W.lcg_states(seed, pool), kind="stable").astype(np.int32)
+    k_pages = np.zeros((pool, Hkv, 16, D), np.int8)
+    v_pages = np.zeros((pool, Hkv, D, 16), np.int8)
+    ks_pages = np.zeros((pool, Hkv, 16), np.float32)
+    vs_pages = np.zeros((pool, Hkv, 16), np.float32)
+    max_blocks = Lmax // 16
+    table = np.full((B, max_blocks), -7, np.int32)  # unused entries hold junk
+    nxt = 0
+    for b in range(B):
+        for i in range(npages[b]):
+            pg = order[nxt]
+            nxt += 1
+            table[b, i] = pg
+            k_pages[pg] = kq[b, :, 16 * i:16 * i + 16]
+            v_pages[pg] = vq[b, :, 16 * i:16 * i + 16].transpose(0, 2, 1)
+            ks_pages[pg] = ks[b, :, 16 * i:16 * i + 16]
+            vs_pages[pg] = vs[b, :, 16 * i:16 * i + 16]
+    return k_pages, v_pages, ks_pages, vs_pages, table
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,lens,window", [
+    (5, 8, 1, 128, [512, 37, 1000, 16, 777], 0),
+    (3, 4, 2, 64, [200, 64, 129], 0),
+    (2, 8, 1, 128, [900, 650], 100),
+])
+def test_decode_paged_matches_oracle(reef, B, Hq, Hkv, D, lens, window):
+    max_ctx = ((max(lens) + 63) // 64) * 64
+    case(f"decode paged B{B} Hq{Hq} Hkv{Hkv} D{D} lens{lens} win{window}")
+    qq, qs, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 41 + B, max_ctx)
+    kp, vp, ksp, vsp, table = _paged(kq, ks, vq, vs, lens, 43 + B)
+    scale = 1 / math.sqrt(D)
+    out = reef.attention_decode_paged(gpu(qq), gpu(qs), gpu(kp), gpu(vp), gpu(ksp), gpu(vsp),
+                                      gpu(table), gpu(np.array(lens, np.int32)), window=window,
+                                      softmax_scale=scale)
+    gold = _decode_gold(qq, qs, kq, ks, vq, vs, lens, window, scale)
+    err = np.abs(host(out) - gold).max()
+    print(f"max_abs_err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def test_decode_paged_flags_bad_pages_and_lengths(reef):
+    case("decode paged: out-of-range page and length are reported")
+    B, Hq, Hkv, D, lens = 2, 4, 1, 64, [40, 30]
+    qq, qs, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 51, 64)
+    kp, vp, ksp, vsp, table = _paged(kq, ks, vq, vs, lens, 52)
+    bad = table.copy()
+    bad[1, 0] = 10_000
+    with pytest.raises(reef.InvalidArgument):
+        reef.attention_decode_paged(gpu(qq), gpu(qs), gpu(kp), gpu(vp), gpu(ksp), gpu(vsp),
+                                    gpu(bad), gpu(np.array(lens, np.int32)))
+    with pytest.raises(reef.InvalidArgument):
+        reef.attention_decode_paged(gpu(qq), gpu(qs), gpu(kp), gpu(vp), gpu(ksp), gpu(vsp),
+                                    gpu(table), gpu(np.array([40, 0], np.int32)))
