@@ -1,0 +1,292 @@
+"""Benchmark of the int8 attention path on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+
+Headline (the JSON line's value): causal int8 prefill attention, batch 1, 32
+heads, seq 2048, head_dim 128, per-head scales -- TOPS of algorithmic work
+(4 * head_dim per visible query-key pair) with the int8 inputs resident in HBM.
+One step is one launch of the prefill kernel over the whole batch.
+
+Also reported in the same line: the int8-KV decode configurations (B64 32q/8kv
+L4096 contiguous; B128 8q/1kv ragged L in [512, 8192] over a 16-token paged
+cache) as GB/s of algorithmic bytes against HBM peak, and the Reef engine's CPU
+path (its own functions, compiled from its headers into oracle/_ref) timed on a
+bounded sample of the headline workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "prefill int8 attn TOPS (% MFMA peak); decode KV GB/s (% HBM peak)"
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 matrix peak, TOP/s
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate budget of the CPU-baseline sample")
+    ap.add_argument("--prefill", default="c2", choices=["c1", "c2", "c4", "c5a"],
+                    help="prefill workload to time (c2, the headline, by default)")
+    ap.add_argument("--decode", default="c3,c5b",
+                    help="decode workloads to time (comma list of c3, c5b)")
+    return ap.parse_args()
+
+
+def timed(torch, launch, steps, warmup):
+    """Wall time of exactly `steps` launches between synchronizations, and the mean
+    kernel duration from HIP events recorded around each launch on the stream."""
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in ev:
+        s.record()
+        launch()
+        e.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    kern_ms = float(np.mean([s.elapsed_time(e) for s, e in ev]))
+    return wall_ms, kern_ms
+
+
+def prefill_launcher(torch, reef, cfg, q, k, v, qs, ks, vs, out):
+    """Direct C-ABI call with prebuilt arguments (no per-call Python setup)."""
+    lib = reef.lib()
+    B, Hq, S, D = q.shape
+    gran = reef.PER_HEAD if cfg.granularity == 1 else reef.PER_TENSOR
+    p = reef.AttentionParams(B, Hq, k.shape[1], S, S, D, 0, 0, cfg.softmax_scale, gran, gran, 0)
+    st = lambda t: reef.Strides(t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
+    sq, sk, sv, so = st(q), st(k), st(v), st(out)
+    args = (C.byref(p), C.c_void_p(q.data_ptr()), C.byref(sq), C.c_void_p(k.data_ptr()),
+            C.byref(sk), C.c_void_p(v.data_ptr()), C.byref(sv), C.c_void_p(qs.data_ptr()),
+            C.c_void_p(ks.data_ptr()), C.c_void_p(vs.data_ptr()), C.c_void_p(out.data_ptr()),
+            C.byref(so))
+    fn = lib.reef_attention_prefill_int8
+
+    def launch():
+        rc = fn(*args, C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"prefill status {rc}")
+    return launch
+
+
+def bench_prefill(torch, reef, W, args):
+    cfg = W.CONFIGS[args.prefill]
+    qf, kf, vf = W.device_prefill_inputs(cfg)
+    quantize = reef.quantize_per_head if cfg.granularity == 1 else reef.quantize_per_tensor
+    q, qs = quantize(qf)
+    k, ks = quantize(kf)
+    v, vs = quantize(vf)
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+
+    def quant():  # the quantization of the three tensors, timed on its own
+        quantize(qf)
+        quantize(kf)
+        quantize(vf)
+    _, quant_ms = timed(torch, quant, 5, 2)
+    del qf, kf, vf
+    launch = prefill_launcher(torch, reef, cfg, q, k, v, qs, ks, vs, out)
+    wall_ms, kern_ms = timed(torch, launch, args.steps, args.warmup)
+    if not torch.isfinite(out).all():
+        raise RuntimeError("prefill produced non-finite output")
+    ops = cfg.algorithmic_ops()
+    quant_bytes = (q.numel() + k.numel() + v.numel()) * 5 + 4 * (qs.numel() + ks.numel() + vs.numel())
+    return cfg, ops, wall_ms, kern_ms, quant_ms, quant_bytes, (q, k, v, qs, ks, vs)
+
+
+def decode_c3(torch, reef, W, steps, warmup):
+    cfg = W.CONFIGS["c3"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(cfg.seed)
+    B, Hq, Hkv, D, L = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.context
+    qf = torch.randn((B, Hq, D), generator=g, device="cuda")
+    q, qsc = reef.quantize_rows(qf)
+    kf = torch.randn((B, Hkv, L, D), generator=g, device="cuda")
+    k, ksc = reef.quantize_rows(kf)
+    del kf
+    vf = torch.randn((B, Hkv, L, D), generator=g, device="cuda")
+    vq, vsc = reef.quantize_rows(vf)
+    del vf
+    vp = reef.pack_v_pages(vq)
+    del vq
+    out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
+    status = reef.StatusWord()
+    p = reef._decode_params(q, L, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN, 0)
+    ws = reef.decode_workspace(p, q.device)
+
+    def launch():
+        reef.attention_decode(q, qsc, k, vp, ksc, vsc, None, softmax_scale=1 / math.sqrt(D),
+                              workspace=ws, status=status, out=out)
+    wall_ms, kern_ms = timed(torch, launch, steps, warmup)
+    status.check("decode")
+    return cfg, cfg.kv_bytes(), wall_ms, kern_ms
+
+
+def decode_c5b(torch, reef, W, steps, warmup, pools=3):
+    """Ragged paged decode. The pages of one step (about 150 MB) fit in the 256 MB
+    last-level cache, so steps rotate over `pools` independent page pools."""
+    cfg = W.CONFIGS["c5b"]
+    B, Hq, Hkv, D = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim
+    lens = cfg.lengths()
+    npages = (lens + 15) // 16
+    total = int(npages.sum())
+    pool_pages = int(total * cfg.pool_slack) + 1
+    max_blocks = cfg.context // 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(cfg.seed)
+    qf = torch.randn((B, Hq, D), generator=g, device="cuda")
+    q, qsc = reef.quantize_rows(qf)
+    setups = []
+    for i in range(pools):
+        kf = torch.randn((pool_pages, Hkv, 16, D), generator=g, device="cuda")
+        kp, ksp = reef.quantize_rows(kf)
+        del kf
+        vf = torch.randn((pool_pages, Hkv, 16, D), generator=g, device="cuda")
+        vq, vsp = reef.quantize_rows(vf)
+        del vf
+        vp = reef.pack_v_pages(vq.reshape(pool_pages * Hkv * 16, D)).reshape(pool_pages, Hkv, D, 16)
+        del vq
+        order = np.argsort(W.lcg_states(cfg.seed + 7 + i, pool_pages), kind="stable")
+        table = np.zeros((B, max_blocks), np.int32)
+        at = 0
+        for b in range(B):
+            table[b, : npages[b]] = order[at: at + npages[b]]
+            at += npages[b]
+        setups.append((kp, vp, ksp, vsp, torch.from_numpy(table).cuda()))
+    lens_t = torch.from_numpy(lens.astype(np.int32)).cuda()
+    out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
+    status = reef.StatusWord()
+    p = reef._decode_params(q, max_blocks * 16, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN, 0)
+    ws = reef.decode_workspace(p, q.device)
+    it = [0]
+
+    def launch():
+        kp, vp, ksp, vsp, table = setups[it[0] % pools]
+        it[0] += 1
+        reef.attention_decode_paged(q, qsc, kp, vp, ksp, vsp, table, lens_t,
+                                    softmax_scale=1 / math.sqrt(D), workspace=ws,
+                                    status=status, out=out)
+    wall_ms, kern_ms = timed(torch, launch, steps, warmup)
+    status.check("decode paged")
+    return cfg, cfg.kv_bytes(lens), wall_ms, kern_ms
+
+
+def cpu_baseline(cfg, inputs, budget_s):
+    """The engine's own CPU attention (oracle/_ref, kind "reference") or, when it was
+    not built, the oracle restatement (kind "port"): one thread, whole heads of the
+    headline workload until the time budget is spent; ops per second are scaled
+    from the heads done."""
+    import oracle
+    q, k, v, qs, ks, vs = (t.cpu().numpy() for t in inputs)
+    S, D = cfg.seq, cfg.head_dim
+    kind = "reference" if oracle.ref_available() else "port"
+    heads, t_total = 0, 0.0
+    while t_total < budget_s and heads < cfg.q_heads:
+        h = heads
+        t0 = time.perf_counter()
+        if kind == "reference":
+            oracle.ref_attention_int8_head(q[0, h], k[0, h], v[0, h], np.full(S, qs[h], np.float32),
+                                           np.full(S, ks[h], np.float32),
+                                           np.full(S, vs[h], np.float32), 0, 0, cfg.softmax_scale)
+        else:
+            p = oracle.Problem(1, 1, 1, S, S, D, softmax_scale=cfg.softmax_scale)
+            oracle.attention_int8(p, q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], qs[h:h + 1],
+                                  ks[h:h + 1], vs[h:h + 1], threads=1)
+        t_total += time.perf_counter() - t0
+        heads += 1
+    ops = 4 * D * heads * S * (S + 1) // 2
+    tops = ops / t_total / 1e12
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((l.split(":", 1)[1].strip() for l in f if "model name" in l), "")
+    except OSError:
+        pass
+    return {"value": tops, "unit": "TOPS", "cores": 1, "kind": kind,
+            "sample": f"{heads} of {cfg.q_heads} heads of the headline workload "
+                      f"({t_total:.1f} s, 1 thread, {os.cpu_count()} host cores, {cpu_model})",
+            "seconds_full_workload_extrapolated": t_total * cfg.q_heads / heads}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import reef_amd as reef
+    from reef_amd import workloads as W
+
+    reef.lib()
+    cfg, ops, wall_ms, kern_ms, quant_ms, quant_bytes, inputs = bench_prefill(torch, reef, W,
+                                                                              args)
+    value = ops / (wall_ms * 1e-3) / 1e12
+    achieved = ops / (kern_ms * 1e-3) / 1e12
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: N(0,1) fp32 drawn on the GPU from a fixed seed, quantized per head "
+                "to int8 by the library before timing",
+        "config": {"workload": cfg.name, "batch": cfg.batch, "q_heads": cfg.q_heads,
+                   "kv_heads": cfg.kv_heads, "seq_len": cfg.seq, "head_dim": cfg.head_dim,
+                   "causal": True, "scales": "per-head"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                     "traffic": None, "kernel": "prefill_kernel<128, false, false>",
+                     "kernel_ms": round(kern_ms, 5), "algorithmic_ops_per_launch": ops},
+        "quantize": {"kernels": "quantize of q, k, v (3 x (zero, max, quantize, scale))",
+                     "ms": round(quant_ms, 4),
+                     "GB/s": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1)},
+    }
+    if not args.no_decode:
+        dec = []
+        fns = {"c3": decode_c3, "c5b": decode_c5b}
+        for fn in (fns[n] for n in args.decode.split(",") if n):
+            dcfg, nbytes, dwall, dkern = fn(torch, reef, W, max(10, args.steps // 2), 5)
+            gbs = nbytes / (dkern * 1e-3) / 1e9
+            dec.append({"workload": dcfg.name, "bytes_per_step": nbytes,
+                        "ms_per_step": round(dwall, 5), "kernel_ms": round(dkern, 5),
+                        "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                        "GB/s_wall": round(nbytes / (dwall * 1e-3) / 1e9, 1)})
+            torch.cuda.empty_cache()
+        rec["decode"] = dec
+    if not args.no_cpu:
+        rec["cpu_baseline"] = cpu_baseline(cfg, inputs, args.cpu_seconds)
+    else:
+        rec["cpu_baseline"] = None
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

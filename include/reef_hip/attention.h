@@ -116,7 +116,7 @@ typedef struct reef_attention_params {
     int64_t q_len, kv_len, head_dim;  /* head_dim 64 or 128 */
     int64_t query_start; /* position of query row 0; engine: kv_len - q_len (attention.hpp:415) */
     int64_t window;      /* 0: GlobalAttention; > 0: LocalAttention window (attention.hpp:223-261) */
-    float softmax_scale;
+    float softmax_scale;    /* > 0; scales must be positive, as the quantizers make them */
     int32_t q_granularity;  /* reef_scale_granularity of q_scales */
     int32_t kv_granularity; /* reef_scale_granularity of k_scales and v_scales */
     uint32_t flags;

@@ -14,10 +14,11 @@
 //   * S^T = K . q^T on v_mfma_i32_16x16x64_i8: a 16-key x 16-head block per
 //     instruction; lane group g of the output holds keys 16g + 4t + i, i.e. the
 //     whole 16-token page g of the 64-key block.
-//   * out = P . V on v_mfma_f32_16x16x32_f16: P comes from the score registers
-//     unchanged (page g's 16 keys are lane group g's P operand), and V pages are
-//     stored transposed ([D, 16] per page), so a lane's V operand for one channel
-//     and 16 keys is one 16-byte load, converted exactly to fp16.
+//   * out^T = V^T . P^T on v_mfma_f32_16x16x32_f16: P comes from the score
+//     registers unchanged (page g's 16 keys are lane group g's P operand), and V
+//     pages are stored transposed ([D, 16] per page), so a lane's V operand for
+//     one channel and 16 keys is one 16-byte load, converted exactly to fp16.
+//     The head stays in lane % 16 from scores to output.
 // Only G = q_heads / kv_heads of the 16 instruction columns are live (4 for
 // 4:1 grouping); the instructions are far from the bound, HBM is.
 #include <algorithm>
@@ -222,14 +223,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
             l_run += p;
             pop[r >> 3][r & 7] = (_Float16)(p * (vv[r] * inv_s));
         }
-        // The 16x16 instruction's rows are heads, so the P operand is laid out
-        // with the head in lane % 16 -- which is where the score output put it.
+        // out^T = V^T . P^T: the output column is the head (lane % 16), the lane
+        // that owns the head's running max, so the rescale above is per lane.
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
             f16x8 v0, v1;
             int8x16_to_f16(vop[d], v0, v1);
-            acc[d] = mfma_16x16x32_f16(pop[0], v0, acc[d]);
-            acc[d] = mfma_16x16x32_f16(pop[1], v1, acc[d]);
+            acc[d] = mfma_16x16x32_f16(v0, pop[0], acc[d]);
+            acc[d] = mfma_16x16x32_f16(v1, pop[1], acc[d]);
         }
     }
     if (bad_page) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
@@ -237,15 +238,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
     // Row sums: this lane holds head col's partial over its 16 keys per block.
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
-    // acc[d][i] is (head 4 grp + i, channel 16 d + col); write live heads.
+    // acc[d][i] is (channel 16 d + 4 grp + i, head col); write live heads.
     const int64_t base_bh = (int64_t)b * a.q_heads + kvh * a.group;
+    if (head_ok) {
+        float *po = a.part_o + ((base_bh + col) * a.splits + split) * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int hh = 4 * grp + i;
-        if (hh >= a.group) continue;
-        float *po = a.part_o + ((base_bh + hh) * a.splits + split) * D;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) po[16 * d + col] = acc[d][i] * s_run;
+        for (int d = 0; d < DB; ++d)
+            *reinterpret_cast<f32x4 *>(po + 16 * d + 4 * grp) = acc[d] * s_run;
     }
     if (head_ok && grp == 0) {
         float *ml = a.part_ml + ((base_bh + col) * a.splits + split) * 2;

@@ -21,6 +21,8 @@
 //     masking runs only on tiles that cross a boundary.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <type_traits>
 
 #include "reef_common.hpp"
 
@@ -41,6 +43,7 @@ struct PrefillArgs {
     float score_scale;  // softmax_scale * log2(e)
     int32_t q_gran, kv_gran;
     int32_t q_tiles;
+    int32_t zigzag;  // pair heavy and light tiles in grids that fit at once
 };
 
 // Row m of a 32-row score block holds key sigma(m) = 16 ((m >> 2) & 1) +
@@ -85,20 +88,55 @@ __device__ __forceinline__ float scale_of(const float *s, int gran, int b, int h
     return s[((int64_t)b * heads + h) * tokens + t];
 }
 
+// Two fp16 of keys (key0, key1) at one channel from the int8 bytes b0 (of key0)
+// and b1 (of key1) at byte `sel` of words w0 and w1 (already XORed with 0x80):
+// the byte gather leaves [b0, 0, b1, 0]; the 0x64 exponent bytes make each half
+// the fp16 1024 + (b + 128), and subtracting 1152 gives b exactly.
+__device__ __forceinline__ f16x2 int8_pair_to_f16(uint32_t w0, uint32_t w1, int sel) {
+    const uint32_t pick = (uint32_t)sel | (0x0cu << 8) | ((uint32_t)(4 + sel) << 16) | (0x0cu << 24);
+    const uint32_t bits = __builtin_amdgcn_perm(w1, w0, pick) | 0x64006400u;
+    return __builtin_bit_cast(f16x2, bits) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+
+// Logical rank of this workgroup's (query tile, batch x head) item. Ranks are
+// heaviest first (the causal rows of the last tile see the most keys). With
+// zig-zag on, the second half of the grid takes ranks in reverse, so that the
+// two workgroups a compute unit receives in a grid that fits at once are a heavy
+// and a light tile.
+__device__ __forceinline__ void work_item(const PrefillArgs &a, int &tile, int &b, int &h) {
+    const int L = blockIdx.x, N = gridDim.x;
+    int rank = L;
+    if (a.zigzag) {
+        const int half = (N + 1) / 2;
+        rank = L < half ? L : N - 1 - (L - half);
+    }
+    const int pairs = a.batch * a.q_heads;
+    tile = a.q_tiles - 1 - rank / pairs;
+    const int bh = rank % pairs;
+    b = bh / a.q_heads;
+    h = bh % a.q_heads;
+}
+
 template <int D, bool KV_TOKEN, bool PRECISE>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_kernel(PrefillArgs a) {
     constexpr int KSTRIDE = D + 16;         // bytes per K row in LDS
     constexpr int VSTRIDE = kBN * 2 + 16;   // bytes per transposed-V row in LDS
     constexpr int DB = D / 32;              // 32-wide output blocks
-    __shared__ __attribute__((aligned(16))) int8_t sK[kBN * KSTRIDE];
-    __shared__ __attribute__((aligned(16))) int8_t sVT[D * VSTRIDE];
-    __shared__ float sKS[KV_TOKEN ? kBN : 1], sVS[KV_TOKEN ? kBN : 1];
-    __shared__ float sVmax;
+    constexpr int K_BYTES = kBN * KSTRIDE, V_BYTES = D * VSTRIDE;
+    constexpr int KLOADS = kBN * D / 16 / kThreads;  // 16-byte K loads per thread
+    constexpr int VBLOCKS = (kBN / 4) * (D / 8);     // 4-key x 8-channel V blocks
+    constexpr float kLazy = 8.0f;  // rescale only when a row max grows by > 2^8
+    // Two stages: the tile being computed and the next one being filled.
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * (K_BYTES + V_BYTES)];
+    __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // The wave index is the same on every lane; saying so lets every per-wave
+    // decision below be a scalar branch instead of predicated vector code.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, grp = lane >> 5;
-    const int tile = a.q_tiles - 1 - (int)blockIdx.x;  // long causal rows first
-    const int h = blockIdx.y, b = blockIdx.z;
+    int tile, b, h;
+    work_item(a, tile, b, h);
     const int kvh = h / (a.q_heads / a.kv_heads);
     const int q0 = tile * kBM;
     const int row = q0 + wave * 32 + col;
@@ -111,6 +149,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const float cq = row_ok ? scale_of(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float ck = KV_TOKEN ? 1.0f : scale_of(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
     const float cv = KV_TOKEN ? 1.0f : scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    // log2-domain score per unit of int32 accumulator
     const float c = cq * ck * a.score_scale;
 
     // Visible keys of this lane's row: [lo, hi].
@@ -133,136 +172,249 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int8_t *kbase = a.k + b * a.k_sb + kvh * a.k_sh;
     const int8_t *vbase = a.v + b * a.v_sb + kvh * a.v_sh;
 
-    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f;
+    // ---- staging: global -> registers (next tile) -> LDS ----------------------------
+    i32x4 kreg[KLOADS];
+    uint2 vreg[4];
+    float ks_reg = 0.0f, vs_reg = 0.0f;
+    // This thread's V block (if tid < VBLOCKS): keys 4 vkg..+3, channels 8 vdg..+7. Key
+    // groups vary fastest, so the 16 lanes storing one transposed row write 128
+    // contiguous bytes (rows 8 channels apart would all hit the same banks).
+    const int vkg = tid % (kBN / 4), vdg = tid / (kBN / 4);
+    // Loads go through buffer resources over this (batch, kv head)'s rows: the
+    // per-lane offsets below never change, the tile offset is a scalar, and keys
+    // past kv_len read zeros (every tile reaching past kv_len is masked anyway).
+    const __amdgpu_buffer_rsrc_t krsrc =
+        buffer_rsrc(kbase, (uint32_t)((int64_t)(a.kv_len - 1) * a.k_st + D));
+    const __amdgpu_buffer_rsrc_t vrsrc =
+        buffer_rsrc(vbase, (uint32_t)((int64_t)(a.kv_len - 1) * a.v_st + D));
+    // K chunk j of this thread: LDS row krow[j] (rows are 144 bytes, so rows r and
+    // r + 8 fill the 64 banks together; they share each 16-lane store group),
+    // holding key kkey of the tile, bytes kch * 16.
+    uint32_t koff[KLOADS];
+    int kdst[KLOADS];
+#pragma unroll
+    for (int j = 0; j < KLOADS; ++j) {
+        const int slot = (tid + j * kThreads) / (D / 16), kch = tid % (D / 16);
+        const int row = (slot & ~9) | ((slot & 1) << 3) | ((slot >> 3) & 1);
+        const int kkey = ((row >> 5) << 5) + key_of_score_row(row & 31);
+        koff[j] = (uint32_t)(kkey * a.k_st + kch * 16);
+        kdst[j] = row * KSTRIDE + kch * 16;
+    }
+    uint32_t voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)((4 * vkg + i) * a.v_st + 8 * vdg);
+    const int64_t srow = ((int64_t)b * a.kv_heads + kvh) * a.kv_len;
+    const __amdgpu_buffer_rsrc_t ksrsrc = buffer_rsrc(a.ks + srow, (uint32_t)a.kv_len * 4u);
+    const __amdgpu_buffer_rsrc_t vsrsrc = buffer_rsrc(a.vs + srow, (uint32_t)a.kv_len * 4u);
+    auto load_tile = [&](int kt) {
+        const int ks_off = __builtin_amdgcn_readfirstlane((int)(kt * a.k_st));
+        const int vs_off = __builtin_amdgcn_readfirstlane((int)(kt * a.v_st));
+#pragma unroll
+        for (int j = 0; j < KLOADS; ++j)
+            kreg[j] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, koff[j], ks_off, 0);
+        if (tid < VBLOCKS) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const auto w = __builtin_amdgcn_raw_buffer_load_b64(vrsrc, voff[i], vs_off, 0);
+                vreg[i] = uint2{w[0], w[1]};
+            }
+        }
+        if (KV_TOKEN && wave == 0) {
+            ks_reg = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(ksrsrc, lane * 4, kt * 4, 0));
+            vs_reg = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(vsrsrc, lane * 4, kt * 4, 0));
+        }
+    };
+    auto store_tile = [&](int buf) {
+        int8_t *sK = smem + buf * (K_BYTES + V_BYTES);
+        int8_t *sVT = sK + K_BYTES;
+#pragma unroll
+        for (int j = 0; j < KLOADS; ++j) *reinterpret_cast<i32x4 *>(sK + kdst[j]) = kreg[j];
+        if (tid < VBLOCKS) {
+            uint32_t w[4][2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w[i][0] = vreg[i].x ^ 0x80808080u;
+                w[i][1] = vreg[i].y ^ 0x80808080u;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const f16x2 k01 = int8_pair_to_f16(w[0][j >> 2], w[1][j >> 2], j & 3);
+                const f16x2 k23 = int8_pair_to_f16(w[2][j >> 2], w[3][j >> 2], j & 3);
+                *reinterpret_cast<f16x4 *>(sVT + (8 * vdg + j) * VSTRIDE + 4 * vkg * 2) =
+                    f16x4{k01[0], k01[1], k23[0], k23[1]};
+            }
+        }
+        if (KV_TOKEN && wave == 0) {
+            sScale[buf][lane] = ks_reg;
+            sScale[buf][kBN + lane] = vs_reg;
+            const float m = wave_max(vs_reg);
+            if (lane == 0) sScale[buf][2 * kBN] = m;
+        }
+    };
+
+    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
 
-    for (int kt = key_lo / kBN * kBN; kt <= key_hi; kt += kBN) {
-        __syncthreads();  // the previous tile's LDS reads are done
-        // K tile -> LDS, rows permuted (score_row_of_key) within each 32-key block.
-        for (int idx = tid; idx < kBN * D / 16; idx += kThreads) {
-            const int kk = idx / (D / 16), ch = idx % (D / 16);
-            const int key = kt + kk;
-            i32x4 val = {0, 0, 0, 0};
-            if (key < a.kv_len)
-                val = *reinterpret_cast<const i32x4 *>(kbase + (int64_t)key * a.k_st + ch * 16);
-            const int r = ((kk >> 5) << 5) + score_row_of_key(kk & 31);
-            *reinterpret_cast<i32x4 *>(sK + r * KSTRIDE + ch * 16) = val;
-        }
-        // V tile -> LDS as fp16, transposed: row d holds the tile's 64 keys.
-        for (int idx = tid; idx < (kBN / 4) * (D / 8); idx += kThreads) {
-            const int kg = idx / (D / 8), dg = idx % (D / 8);
-            uint2 w[4];
+    // One tile of scores, online softmax and P.V for this wave's 32 rows.
+    auto tile_math = [&](const int kt, const int buf, auto mask_tag) {  // wave-uniform
+            const int8_t *sK = smem + buf * (K_BYTES + V_BYTES);
+            constexpr bool need_mask = decltype(mask_tag)::value;
+            const int8_t *sVT = sK + K_BYTES;
+            i32x16 sc[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kt + 4 * kg + i;
-                w[i] = key < a.kv_len
-                           ? *reinterpret_cast<const uint2 *>(vbase + (int64_t)key * a.v_st + 8 * dg)
-                           : uint2{0u, 0u};
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                f16x4 h4;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t word = j < 4 ? w[i].x : w[i].y;
-                    h4[i] = (_Float16)(int)(int8_t)(word >> (8 * (j & 3)));
-                }
-                *reinterpret_cast<f16x4 *>(sVT + (8 * dg + j) * VSTRIDE + 4 * kg * 2) = h4;
-            }
-        }
-        if (KV_TOKEN && wave == 0) {
-            const int key = kt + lane;
-            const int64_t at = ((int64_t)b * a.kv_heads + kvh) * a.kv_len + key;
-            const float ks = key < a.kv_len ? a.ks[at] : 0.0f;
-            const float vs = key < a.kv_len ? a.vs[at] : 0.0f;
-            sKS[lane] = ks;
-            sVS[lane] = vs;
-            const float m = wave_max(vs);
-            if (lane == 0) sVmax = m;
-        }
-        __syncthreads();
-        if (!wave_active || kt > wk_hi || kt + kBN - 1 < wk_lo) continue;  // wave-uniform
-        const bool need_mask = !(kt + kBN - 1 <= full_hi && kt >= full_lo);
+            for (int u = 0; u < 2; ++u)
+                sc[u] = score_tile<D>(qop, sK + (32 * u + col) * KSTRIDE, grp);
 
-        i32x16 sc[2];
+            // Tile max of the log2-domain scores, masked keys excluded.
+            float mt;
+            float x[KV_TOKEN ? 32 : 1];
+            if (KV_TOKEN) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) sc[u] = score_tile<D>(qop, sK + (32 * u + col) * KSTRIDE, grp);
-
-        float x[32];
+                for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kt + 32 * u + 16 * grp + r;
+                        float xv = (float)sc[u][r] * (c * sScale[buf][32 * u + 16 * grp + r]);
+                        if constexpr (need_mask) {
+                            if (key < lo || key > hi) xv = -INFINITY;
+                        }
+                        x[16 * u + r] = xv;
+                    }
+                mt = x[0];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float cs = KV_TOKEN ? c * sKS[32 * u + 16 * grp + r] : c;
-                x[16 * u + r] = (float)sc[u][r] * cs;
-            }
-        }
-        if (need_mask) {
+                for (int r = 1; r < 32; ++r) mt = fmaxf(mt, x[r]);
+            } else {
+                if constexpr (need_mask) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+                    for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kt + 32 * u + 16 * grp + r;
-                    if (key < lo || key > hi) x[16 * u + r] = -INFINITY;
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = kt + 32 * u + 16 * grp + r;
+                            if (key < lo || key > hi) sc[u][r] = INT32_MIN;
+                        }
                 }
+                int mi = sc[0][0];
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc[u][r]);
+                // c > 0, so the largest float score is c times the largest integer.
+                mt = mi == INT32_MIN ? -INFINITY : (float)mi * c;
             }
-        }
-        float mt = x[0];
-#pragma unroll
-        for (int r = 1; r < 32; ++r) mt = fmaxf(mt, x[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float alpha_o = alpha, inv_s = 1.0f;
-        if (KV_TOKEN) {
-            // Values are accumulated in units of s_run, the largest value scale
-            // seen so far, so that p * v_scale / s_run stays in [0, 1].
-            const float s_new = fmaxf(s_run, sVmax);
-            alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
-            inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
-            s_run = s_new;
-        }
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
-
-        f16x8 phi[2][2], plo[2][2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int r = 8 * s + e;
-                    const float p = __builtin_amdgcn_exp2f(x[16 * u + r] - m_use);
-                    l_run += p;
-                    const float pv = KV_TOKEN ? p * (sVS[32 * u + 16 * grp + r] * inv_s) : p;
-                    const _Float16 hi16 = (_Float16)pv;
-                    phi[u][s][e] = hi16;
-                    if (PRECISE) plo[u][s][e] = (_Float16)(pv - (float)hi16);
+            mt = xor32_max(mt);
+            float svt = 0.0f;
+            bool grow = mt > m_run + kLazy;
+            if (KV_TOKEN) {
+                svt = sScale[buf][2 * kBN];
+                grow = grow || svt > s_run * 16.0f;
+            }
+            // Lazy rescale: the running max only moves when some row's max grows by
+            // more than 2^kLazy (exp values stay <= 2^8, well inside fp16).
+            if (__any(grow)) {
+                const float m_new = fmaxf(m_run, mt);
+                float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+                float alpha_o = alpha;
+                if (KV_TOKEN) {
+                    // Values accumulate in units of s_run, the largest value scale so
+                    // far, so that p * v_scale / s_run stays bounded in fp16.
+                    const float s_new = fmaxf(s_run, svt);
+                    alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
+                    inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
+                    s_run = s_new;
                 }
-            }
-        }
+                m_run = m_new;
+                l_run *= alpha;
 #pragma unroll
-        for (int d = 0; d < DB; ++d) {
+                for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
+            }
+
+            f16x8 phi[2][2], plo[2][2];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const f16x8 vop = *reinterpret_cast<const f16x8 *>(
-                        sVT + (32 * d + col) * VSTRIDE + (32 * u + 16 * grp + 8 * s) * 2);
-                    acc[d] = mfma_32x32x16_f16(vop, phi[u][s], acc[d]);
-                    if (PRECISE) acc[d] = mfma_32x32x16_f16(vop, plo[u][s], acc[d]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int r = 8 * s + e;
+                        float p;
+                        if (KV_TOKEN) {
+                            // A row with nothing visible yet keeps m_run = -inf.
+                            p = __builtin_amdgcn_exp2f(x[16 * u + r] - m_run);
+                            if constexpr (need_mask) {
+                                if (x[16 * u + r] == -INFINITY) p = 0.0f;
+                            }
+                        } else {
+                            p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[u][r], c, -m_run));
+                            if constexpr (need_mask) {
+                                if (sc[u][r] == INT32_MIN) p = 0.0f;
+                            }
+                        }
+                        if (KV_TOKEN) l_run += p;
+                        const float pv =
+                            KV_TOKEN ? p * (sScale[buf][kBN + 32 * u + 16 * grp + r] * inv_s) : p;
+                        const _Float16 hi16 = (_Float16)pv;
+                        phi[u][s][e] = hi16;
+                        if (PRECISE) plo[u][s][e] = (_Float16)(pv - (float)hi16);
+                    }
+                    if (!KV_TOKEN) {
+                        // Row sum of the fp16 probabilities the P.V product uses, two
+                        // per instruction, accumulated in fp32.
+                        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2) {
+                            const f16x2 pr = {phi[u][s][e], phi[u][s][e + 1]};
+                            l_run = __builtin_amdgcn_fdot2(pr, one, l_run, false);
+                            if (PRECISE) {
+                                const f16x2 pl = {plo[u][s][e], plo[u][s][e + 1]};
+                                l_run = __builtin_amdgcn_fdot2(pl, one, l_run, false);
+                            }
+                        }
+                    }
                 }
             }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    f16x8 vop[DB];
+#pragma unroll
+                    for (int d = 0; d < DB; ++d)
+                        vop[d] = *reinterpret_cast<const f16x8 *>(
+                            sVT + (32 * d + col) * VSTRIDE + (32 * u + 16 * grp + 8 * s) * 2);
+#pragma unroll
+                    for (int d = 0; d < DB; ++d) {
+                        acc[d] = mfma_32x32x16_f16(vop[d], phi[u][s], acc[d]);
+                        if (PRECISE) acc[d] = mfma_32x32x16_f16(vop[d], plo[u][s], acc[d]);
+                    }
+                }
+            }
+            };
+
+    const int kt0 = key_lo / kBN * kBN;
+    const int n_tiles = (key_hi - kt0) / kBN + 1;
+    load_tile(kt0);
+    store_tile(0);
+    __syncthreads();
+    for (int it = 0; it < n_tiles; ++it) {
+        const int kt = kt0 + it * kBN;
+        const int buf = it & 1;
+        if (it + 1 < n_tiles) load_tile(kt + kBN);  // in flight during this tile's math
+        if (wave_active && kt <= wk_hi && kt + kBN - 1 >= wk_lo) {  // wave-uniform
+            // Tiles inside every row's visible range take the path without masks.
+            if (kt + kBN - 1 <= full_hi && kt >= full_lo)
+                tile_math(kt, buf, std::false_type{});
+            else
+                tile_math(kt, buf, std::true_type{});
         }
+        if (it + 1 < n_tiles) store_tile(buf ^ 1);
+        __syncthreads();
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float l_tot = xor32_sum(l_run);
     if (!row_ok) return;
     const float norm = (KV_TOKEN ? s_run : cv) / l_tot;
     float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
@@ -336,12 +488,17 @@ extern "C" reef_status reef_attention_prefill_int8(
         p->kv_len <= 0 || D <= 0 || p->q_heads % p->kv_heads != 0 || p->query_start < 0 ||
         p->window < 0 || p->query_start + p->q_len > p->kv_len ||
         !valid_granularity(p->q_granularity) || !valid_granularity(p->kv_granularity) ||
-        !std::isfinite(p->softmax_scale))
+        !std::isfinite(p->softmax_scale) || !(p->softmax_scale > 0.0f))
         return REEF_INVALID_ARGUMENT;
     if (p->kv_len >= (int64_t(1) << 30) || p->window >= (int64_t(1) << 30) ||
         p->q_heads > 65535 || p->batch > 65535)
         return REEF_UNSUPPORTED;
     if (D != 64 && D != 128) return REEF_UNSUPPORTED;
+    {
+        // Per-head K/V slices are addressed with 32-bit offsets.
+        const int64_t kst = k_strides ? k_strides->token : D, vst = v_strides ? v_strides->token : D;
+        if ((p->kv_len - 1) * std::max(kst, vst) + D >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
+    }
     if (!valid_int8_strides(q_strides, q) || !valid_int8_strides(k_strides, k) ||
         !valid_int8_strides(v_strides, v) || !aligned(out, 16))
         return REEF_INVALID_ARGUMENT;
@@ -382,8 +539,13 @@ extern "C" reef_status reef_attention_prefill_int8(
     a.q_gran = p->q_granularity;
     a.kv_gran = p->kv_granularity;
     a.q_tiles = (int32_t)ceil_div(Sq, kBM);
+    const int64_t items = a.q_tiles * Hq * p->batch;
+    if (items >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
+    // Two workgroups fit on each of the 256 compute units at once.
+    const char *zz = getenv("REEF_PREFILL_ZIGZAG");
+    a.zigzag = zz ? atoi(zz) : (items <= 512 ? 1 : 0);
 
-    const dim3 grid((unsigned)a.q_tiles, (unsigned)Hq, (unsigned)p->batch);
+    const dim3 grid((unsigned)items);
     const bool tok = p->kv_granularity == REEF_SCALE_PER_TOKEN;
     const bool precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0;
 #define REEF_PREFILL_LAUNCH(DIM, TOK, PREC)                                                  \

@@ -62,6 +62,25 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
+// max / sum of x over lanes l and l ^ 32, in one VALU op (v_permlane32_swap).
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                   false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                   false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// A raw buffer resource over [base, base + bytes): loads through it take a
+// per-lane VGPR offset and a uniform SGPR offset, and read zeros past the end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
 // Scale of quant.hpp:51-57 from a largest magnitude: max / 127 (IEEE
 // division), or 1 when every value was zero.
 __device__ __forceinline__ float int8_scale(float max_magnitude) {
