@@ -62,8 +62,10 @@ __device__ __forceinline__ int key_of_score_row(int m) {
 // bit-exact score hook.
 template <int D>
 __device__ __forceinline__ i32x16 score_tile(const i32x4 (&qop)[D / 32], const int8_t *krow,
-                                             int grp) {
-    i32x16 s = {};
+                                             int grp, int32_t init = 0) {
+    i32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = init;
 #pragma unroll
     for (int t = 0; t < D / 32; ++t) {
         const i32x4 kop = *reinterpret_cast<const i32x4 *>(krow + 32 * t + 16 * grp);
@@ -117,18 +119,37 @@ __device__ __forceinline__ void work_item(const PrefillArgs &a, int &tile, int &
     h = bh % a.q_heads;
 }
 
-template <int D, bool KV_TOKEN, bool PRECISE>
-__global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_kernel(PrefillArgs a) {
-    constexpr int KSTRIDE = D + 16;         // bytes per K row in LDS
-    constexpr int VSTRIDE = kBN * 2 + 16;   // bytes per transposed-V row in LDS
-    constexpr int DB = D / 32;              // 32-wide output blocks
-    constexpr int K_BYTES = kBN * KSTRIDE, V_BYTES = D * VSTRIDE;
+// LDS of one prefill workgroup: two stages (the tile being computed and the next
+// one being filled) of a K tile and a transposed fp16 V tile.
+template <int D>
+struct PrefillLds {
+    static constexpr int KSTRIDE = D + 16;        // bytes per K row
+    static constexpr int VSTRIDE = kBN * 2 + 16;  // bytes per transposed-V row
+    static constexpr int K_BYTES = kBN * KSTRIDE, V_BYTES = D * VSTRIDE;
+    static constexpr int BYTES = 2 * (K_BYTES + V_BYTES);
+};
+
+// Without per-token K scales the score accumulators start at the bits of the
+// float 1.5 * 2^23, so each one reads directly as the float 1.5 * 2^23 + acc
+// (exact: |acc| <= 127 * 127 * 128 < 2^22) and no conversion instruction is
+// needed: p = exp2(t * c - M) with M = m + 1.5 * 2^23 * c rounded once. The
+// rounding of M shifts every exponent of a row by the same amount until the next
+// rescale, and the rescale factor is taken from the M values, so the shift
+// cancels in the normalization. It stays small enough for fp16 (|shift| <=
+// ulp(M) / 2 <= 4) while c < 8; a workgroup with a larger c converts instead.
+constexpr int32_t kBiasBits = 0x4B400000;
+constexpr float kBias = 12582912.0f;
+constexpr float kBiasMaxScale = 8.0f;
+
+template <int D, bool KV_TOKEN, bool PRECISE, bool BIASED>
+__device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
+                                             float (*sScale)[KV_TOKEN ? 2 * kBN + 1 : 1]) {
+    constexpr int KSTRIDE = PrefillLds<D>::KSTRIDE, VSTRIDE = PrefillLds<D>::VSTRIDE;
+    constexpr int DB = D / 32;  // 32-wide output blocks
+    constexpr int K_BYTES = PrefillLds<D>::K_BYTES, V_BYTES = PrefillLds<D>::V_BYTES;
     constexpr int KLOADS = kBN * D / 16 / kThreads;  // 16-byte K loads per thread
     constexpr int VBLOCKS = (kBN / 4) * (D / 8);     // 4-key x 8-channel V blocks
     constexpr float kLazy = 8.0f;  // rescale only when a row max grows by > 2^8
-    // Two stages: the tile being computed and the next one being filled.
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * (K_BYTES + V_BYTES)];
-    __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     // The wave index is the same on every lane; saying so lets every per-wave
@@ -255,6 +276,9 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
     };
 
     float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
+    // m_run + bias * c, rounded: the offset the biased scores are exponentiated at.
+    const float bias = BIASED ? kBias : 0.0f;
+    float big_run = -INFINITY;
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
@@ -267,7 +291,8 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
             i32x16 sc[2];
 #pragma unroll
             for (int u = 0; u < 2; ++u)
-                sc[u] = score_tile<D>(qop, sK + (32 * u + col) * KSTRIDE, grp);
+                sc[u] = score_tile<D>(qop, sK + (32 * u + col) * KSTRIDE, grp,
+                                      KV_TOKEN ? 0 : kBiasBits);
 
             // Tile max of the log2-domain scores, masked keys excluded.
             float mt;
@@ -303,7 +328,7 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
 #pragma unroll
                     for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc[u][r]);
                 // c > 0, so the largest float score is c times the largest integer.
-                mt = mi == INT32_MIN ? -INFINITY : (float)mi * c;
+                mt = mi == INT32_MIN ? -INFINITY : (__int_as_float(mi) - kBias) * c;
             }
             mt = xor32_max(mt);
             float svt = 0.0f;
@@ -325,6 +350,12 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
                     alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
                     inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
                     s_run = s_new;
+                }
+                if (!KV_TOKEN) {
+                    const float big_new = __builtin_fmaf(bias, c, m_new);
+                    alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(big_run - big_new);
+                    alpha_o = alpha;
+                    big_run = big_new;
                 }
                 m_run = m_new;
                 l_run *= alpha;
@@ -348,7 +379,9 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
                                 if (x[16 * u + r] == -INFINITY) p = 0.0f;
                             }
                         } else {
-                            p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[u][r], c, -m_run));
+                            const float t = BIASED ? __int_as_float(sc[u][r])
+                                                   : (float)(sc[u][r] - kBiasBits);
+                            p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, c, -big_run));
                             if constexpr (need_mask) {
                                 if (sc[u][r] == INT32_MIN) p = 0.0f;
                             }
@@ -428,6 +461,27 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
             *reinterpret_cast<f32x4 *>(orow + 32 * d + 8 * j + 4 * grp) = o;
         }
     }
+}
+
+template <int D, bool KV_TOKEN, bool PRECISE>
+__global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
+    __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
+    bool convert = KV_TOKEN;
+    if (!KV_TOKEN) {
+        // The largest log2-domain score scale of the workgroup's rows.
+        int tile, b, h;
+        work_item(a, tile, b, h);
+        const int kvh = h / (a.q_heads / a.kv_heads);
+        const int row = tile * kBM + (int)threadIdx.x / 2;
+        const float cq = row < a.q_len ? scale_of(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
+        const float ck = scale_of(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+        convert = __syncthreads_or(!(cq * ck * a.score_scale < kBiasMaxScale));
+    }
+    if (convert)
+        prefill_body<D, KV_TOKEN, PRECISE, false>(a, smem, sScale);
+    else
+        prefill_body<D, KV_TOKEN, PRECISE, true>(a, smem, sScale);
 }
 
 // Bit-exact hook: the int32 score accumulators, through score_tile. One wave
