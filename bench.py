@@ -1,6 +1,8 @@
 """Benchmark of the int8 attention path on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+python bench.py --profile-pass   (a few launches of every timed kernel and of a plain
+                                  copy of known size, for hardware-counter runs)
 
 Headline (the JSON line's value): causal int8 prefill attention, batch 1, 32
 heads, seq 2048, head_dim 128, per-head scales -- TOPS of algorithmic work
@@ -20,6 +22,7 @@ import ctypes as C
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -46,26 +49,28 @@ def parse():
                     help="prefill workload to time (c2, the headline, by default)")
     ap.add_argument("--decode", default="c3,c5b",
                     help="decode workloads to time (comma list of c3, c5b)")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="run COPY_LAUNCHES copies of COPY_BYTES, then 3 launches of each "
+                         "kernel, and exit (for rocprofv3 --pmc runs)")
     return ap.parse_args()
 
 
 def timed(torch, launch, steps, warmup):
-    """Wall time of exactly `steps` launches between synchronizations, and the mean
-    kernel duration from HIP events recorded around each launch on the stream."""
+    """Wall time per launch of exactly `steps` back-to-back launches between
+    synchronizations, and the GPU time per launch from two HIP events recorded on
+    the launch stream around the same region."""
     for _ in range(warmup):
         launch()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for s, e in ev:
-        s.record()
+    start.record()
+    for _ in range(steps):
         launch()
-        e.record()
+    end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    kern_ms = float(np.mean([s.elapsed_time(e) for s, e in ev]))
+    kern_ms = start.elapsed_time(end) / steps
     return wall_ms, kern_ms
 
 
@@ -191,6 +196,33 @@ def decode_c5b(torch, reef, W, steps, warmup, pools=3):
     return cfg, cfg.kv_bytes(lens), wall_ms, kern_ms
 
 
+COPY_BYTES = 1 << 30  # the calibration copy reads and writes this many bytes
+COPY_LAUNCHES = 3
+
+
+def copy_calibration(torch):
+    """A plain elementwise copy (negation) of COPY_BYTES fp32 bytes: its FETCH_SIZE and
+    WRITE_SIZE counters against the known bytes give the scale of those counters."""
+    x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(COPY_LAUNCHES):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+
+
+def recorded_traffic(workload):
+    """HBM bytes per prefill launch measured by the hardware counters and recorded
+    in profiles/ (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration)."""
+    path = os.path.join(ROOT, "profiles", f"prefill_{workload}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
+
+
 def cpu_baseline(cfg, inputs, budget_s):
     """The engine's own CPU attention (oracle/_ref, kind "reference") or, when it was
     not built, the oracle restatement (kind "port"): one thread, whole heads of the
@@ -240,6 +272,16 @@ def main():
     from reef_amd import workloads as W
 
     reef.lib()
+    if args.profile_pass:
+        copy_calibration(torch)
+        args.steps, args.warmup = 3, 1
+        bench_prefill(torch, reef, W, args)
+        fns = {"c3": decode_c3, "c5b": decode_c5b}
+        for fn in (fns[n] for n in args.decode.split(",") if n):
+            fn(torch, reef, W, 3, 1)
+        print(json.dumps({"profile_pass": True, "copy_bytes": COPY_BYTES,
+                          "copy_launches": COPY_LAUNCHES}), flush=True)
+        return
     cfg, ops, wall_ms, kern_ms, quant_ms, quant_bytes, inputs = bench_prefill(torch, reef, W,
                                                                               args)
     value = ops / (wall_ms * 1e-3) / 1e12
@@ -263,7 +305,8 @@ def main():
                    "causal": True, "scales": "per-head"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                     "traffic": None, "kernel": "prefill_kernel<128, false, false>",
+                     "traffic": recorded_traffic(args.prefill),
+                     "kernel": "prefill_kernel<128, false, false>",
                      "kernel_ms": round(kern_ms, 5), "algorithmic_ops_per_launch": ops},
         "quantize": {"kernels": "quantize of q, k, v (3 x (zero, max, quantize, scale))",
                      "ms": round(quant_ms, 4),

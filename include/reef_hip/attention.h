@@ -55,6 +55,7 @@ typedef enum reef_status {
 #define REEF_STATUS_BIT_NON_FINITE 0x1u
 #define REEF_STATUS_BIT_BAD_PAGE 0x2u
 #define REEF_STATUS_BIT_BAD_LENGTH 0x4u
+#define REEF_STATUS_BIT_CAPACITY 0x8u
 
 typedef enum reef_scale_granularity {
     REEF_SCALE_PER_TENSOR = 0, /* one scale: scales[0] */
@@ -100,8 +101,9 @@ reef_status reef_dequantize_int8(const int8_t *q, int64_t n, int64_t group, cons
                                  float *x, hipStream_t stream);
 
 /* Waits for the stream, reads a status word written by the kernels and maps
- * it: 0 -> REEF_OK, NON_FINITE -> REEF_NON_FINITE_INPUT, page/length bits ->
- * REEF_INVALID_ARGUMENT. Clears the word afterwards when clear != 0. */
+ * it: 0 -> REEF_OK, NON_FINITE -> REEF_NON_FINITE_INPUT, CAPACITY ->
+ * REEF_CAPACITY, page/length bits -> REEF_INVALID_ARGUMENT (first match in
+ * that order). Clears the word afterwards when clear != 0. */
 reef_status reef_read_status_word(uint32_t *status_word, int clear, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
@@ -196,6 +198,47 @@ reef_status reef_attention_decode_int8_paged(
  * [pages, D, 16]. */
 reef_status reef_kv_pack_v_pages(const int8_t *v_tokens, int64_t pages, int64_t head_dim,
                                  int8_t *v_pages, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * KV-cache append: Attention::append_kv_cache (attention.hpp:290-352) on the
+ * int8 cache above. The new_tokens fresh key and value rows of every sequence,
+ * fp32 [B, Hkv, new_tokens, D] with optional strides (a projection output
+ * [new_tokens, Hkv * D] is {0, D, Hkv * D}), are quantized per token exactly as
+ * quantize_rows (quant.hpp:112-133) quantizes them and written at positions
+ * start_positions[b] .. start_positions[b] + new_tokens - 1 of sequence b, in
+ * place. start_positions: [B] int32 on the device.
+ *   - REEF_CAPACITY (host) when new_tokens > max_context; a sequence whose
+ *     append would pass max_context is not written and sets the CAPACITY bit
+ *     (the engine's length_error, attention.hpp:321-327); a negative start sets
+ *     BAD_LENGTH; a page number outside [0, num_pages) sets BAD_PAGE and skips
+ *     that row.
+ *   - Non-finite values set NON_FINITE (the engine throws before writing; here
+ *     the rows of such a call are unspecified).
+ *   - context_lens (optional, may alias start_positions) receives
+ *     start_positions[b] + new_tokens for every sequence that was written.
+ */
+typedef struct reef_kv_append_params {
+    int64_t batch, kv_heads, head_dim; /* head_dim 64 or 128 */
+    int64_t new_tokens;                /* tokens appended to every sequence */
+    int64_t max_context;               /* capacity per sequence, a multiple of 16 */
+} reef_kv_append_params;
+
+reef_status reef_kv_append_int8(const reef_kv_append_params *p, const float *k_new,
+                                const reef_strides *k_strides, const float *v_new,
+                                const reef_strides *v_strides, const int32_t *start_positions,
+                                int8_t *k_cache, int8_t *v_cache, float *k_scales,
+                                float *v_scales, int32_t *context_lens, uint32_t *status_word,
+                                hipStream_t stream);
+
+/* The same into the paged layout; max_context <= max_blocks_per_seq * 16. */
+reef_status reef_kv_append_int8_paged(const reef_kv_append_params *p, const float *k_new,
+                                      const reef_strides *k_strides, const float *v_new,
+                                      const reef_strides *v_strides,
+                                      const int32_t *start_positions, const int32_t *block_table,
+                                      int64_t max_blocks_per_seq, int64_t num_pages,
+                                      int8_t *k_pages, int8_t *v_pages, float *k_scale_pages,
+                                      float *v_scale_pages, int32_t *context_lens,
+                                      uint32_t *status_word, hipStream_t stream);
 
 #ifdef __cplusplus
 }

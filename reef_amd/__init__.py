@@ -31,7 +31,8 @@ EXPORTS = [
     "reef_quantize_int8_per_token", "reef_dequantize_int8", "reef_read_status_word",
     "reef_attention_prefill_int8", "reef_qk_scores_i32",
     "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
-    "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages",
+    "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages", "reef_kv_append_int8",
+    "reef_kv_append_int8_paged",
 ]
 
 
@@ -82,6 +83,11 @@ class DecodeParams(C.Structure):
                 ("num_splits", C.c_int32), ("flags", C.c_uint32)]
 
 
+class KvAppendParams(C.Structure):
+    _fields_ = [("batch", C.c_int64), ("kv_heads", C.c_int64), ("head_dim", C.c_int64),
+                ("new_tokens", C.c_int64), ("max_context", C.c_int64)]
+
+
 _P = C.c_void_p
 _I64 = C.c_int64
 _SIGS = {
@@ -101,6 +107,11 @@ _SIGS = {
     "reef_attention_decode_int8_paged": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P,
                                          _I64, _I64, _P, _P, _P, C.c_size_t, _P, _P],
     "reef_kv_pack_v_pages": [_P, _I64, _I64, _P, _P],
+    "reef_kv_append_int8": [C.POINTER(KvAppendParams), _P, C.POINTER(Strides), _P,
+                            C.POINTER(Strides), _P, _P, _P, _P, _P, _P, _P, _P],
+    "reef_kv_append_int8_paged": [C.POINTER(KvAppendParams), _P, C.POINTER(Strides), _P,
+                                  C.POINTER(Strides), _P, _P, _I64, _I64, _P, _P, _P, _P, _P,
+                                  _P, _P],
 }
 
 _lib_handle = None
@@ -373,3 +384,60 @@ def pack_v_pages(v_tokens):
     out = torch.empty((*lead, L // PAGE, D, PAGE), dtype=torch.int8, device=src.device)
     check(lib().reef_kv_pack_v_pages(_ptr(src), pages, D, _ptr(out), _stream()), "pack_v_pages")
     return out
+
+
+# --- KV-cache append (attention.hpp:290-352) --------------------------------------------
+
+def _append_inputs(k_new, v_new):
+    torch = _torch()
+    _require(k_new, torch.float32, "k_new")
+    _require(v_new, torch.float32, "v_new")
+    if k_new.shape != v_new.shape or k_new.dim() != 4:
+        raise InvalidArgument("KV cache append shape mismatch")
+    return _strides4(k_new), _strides4(v_new)
+
+
+def kv_append(k_new, v_new, start_positions, k_cache, v_pages, k_scales, v_scales,
+              context_lens=None, status: StatusWord | None = None):
+    """Quantize fp32 rows k_new, v_new [B, Hkv, T, D] per token and write them into
+    the contiguous cache (k_cache [B, Hkv, L, D], v_pages [B, Hkv, L/16, D, 16],
+    scales [B, Hkv, L]) at start_positions[b] + t. context_lens, when given, is set
+    to start_positions + T afterwards (it may be start_positions itself)."""
+    torch = _torch()
+    ks, vs = _append_inputs(k_new, v_new)
+    B, H, T, D = k_new.shape
+    L = k_cache.shape[2]
+    if tuple(k_cache.shape) != (B, H, L, D) or v_pages.numel() != k_cache.numel():
+        raise InvalidArgument("KV cache append shape mismatch")
+    _require(start_positions, torch.int32, "start_positions")
+    p = KvAppendParams(B, H, D, T, L)
+    own = status or StatusWord(k_new.device)
+    check(lib().reef_kv_append_int8(
+        C.byref(p), _ptr(k_new), C.byref(ks), _ptr(v_new), C.byref(vs), _ptr(start_positions),
+        _ptr(k_cache), _ptr(v_pages), _ptr(k_scales), _ptr(v_scales), _ptr(context_lens),
+        own.ptr, _stream()), "kv_append")
+    if status is None:
+        own.check("kv_append")
+
+
+def kv_append_paged(k_new, v_new, start_positions, block_table, k_pages, v_pages,
+                    k_scale_pages, v_scale_pages, context_lens=None,
+                    status: StatusWord | None = None, max_context=None):
+    """kv_append into the paged cache (k_pages [P, Hkv, 16, D], v_pages [P, Hkv, D, 16],
+    scale pages [P, Hkv, 16], block_table [B, max_blocks] int32)."""
+    torch = _torch()
+    ks, vs = _append_inputs(k_new, v_new)
+    B, H, T, D = k_new.shape
+    P = k_pages.shape[0]
+    max_blocks = block_table.shape[1]
+    _require(start_positions, torch.int32, "start_positions")
+    _require(block_table, torch.int32, "block_table")
+    p = KvAppendParams(B, H, D, T, max_context or max_blocks * PAGE)
+    own = status or StatusWord(k_new.device)
+    check(lib().reef_kv_append_int8_paged(
+        C.byref(p), _ptr(k_new), C.byref(ks), _ptr(v_new), C.byref(vs), _ptr(start_positions),
+        _ptr(block_table.contiguous()), max_blocks, P, _ptr(k_pages), _ptr(v_pages),
+        _ptr(k_scale_pages), _ptr(v_scale_pages), _ptr(context_lens), own.ptr, _stream()),
+        "kv_append_paged")
+    if status is None:
+        own.check("kv_append_paged")
