@@ -111,7 +111,8 @@ reef_status reef_read_status_word(uint32_t *status_word, int clear, hipStream_t 
  */
 
 /* Attention flags. */
-#define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts */
+#define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts (always on
+                                     * with PER_TOKEN K/V scales) */
 
 typedef struct reef_attention_params {
     int64_t batch, q_heads, kv_heads; /* q head h reads kv head h / (q_heads / kv_heads) */

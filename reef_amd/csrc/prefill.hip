@@ -62,10 +62,8 @@ __device__ __forceinline__ int key_of_score_row(int m) {
 // bit-exact score hook.
 template <int D>
 __device__ __forceinline__ i32x16 score_tile(const i32x4 (&qop)[D / 32], const int8_t *krow,
-                                             int grp, int32_t init = 0) {
-    i32x16 s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = init;
+                                             int grp) {
+    i32x16 s = {};
 #pragma unroll
     for (int t = 0; t < D / 32; ++t) {
         const i32x4 kop = *reinterpret_cast<const i32x4 *>(krow + 32 * t + 16 * grp);
@@ -100,23 +98,26 @@ __device__ __forceinline__ f16x2 int8_pair_to_f16(uint32_t w0, uint32_t w1, int 
     return __builtin_bit_cast(f16x2, bits) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
 }
 
-// Logical rank of this workgroup's (query tile, batch x head) item. Ranks are
-// heaviest first (the causal rows of the last tile see the most keys). With
-// zig-zag on, the second half of the grid takes ranks in reverse, so that the
-// two workgroups a compute unit receives in a grid that fits at once are a heavy
-// and a light tile.
-__device__ __forceinline__ void work_item(const PrefillArgs &a, int &tile, int &b, int &h) {
-    const int L = blockIdx.x, N = gridDim.x;
-    int rank = L;
-    if (a.zigzag) {
-        const int half = (N + 1) / 2;
-        rank = L < half ? L : N - 1 - (L - half);
-    }
+// Work items are (query tile, batch x head), ranked heaviest first: the causal
+// rows of the last tile see the most keys.
+__device__ __forceinline__ void item_coords(const PrefillArgs &a, int rank, int &tile, int &b,
+                                            int &h) {
     const int pairs = a.batch * a.q_heads;
     tile = a.q_tiles - 1 - rank / pairs;
     const int bh = rank % pairs;
     b = bh / a.q_heads;
     h = bh % a.q_heads;
+}
+
+// Rank of this workgroup's item in the one-item-per-workgroup kernel. With
+// zig-zag on, the second half of the grid takes ranks in reverse, so that the
+// two workgroups a compute unit receives in a grid that fits at once are a heavy
+// and a light tile.
+__device__ __forceinline__ int grid_rank(const PrefillArgs &a) {
+    const int L = blockIdx.x, N = gridDim.x;
+    if (!a.zigzag) return L;
+    const int half = (N + 1) / 2;
+    return L < half ? L : N - 1 - (L - half);
 }
 
 // LDS of one prefill workgroup: two stages (the tile being computed and the next
@@ -129,21 +130,16 @@ struct PrefillLds {
     static constexpr int BYTES = 2 * (K_BYTES + V_BYTES);
 };
 
-// Without per-token K scales the score accumulators start at the bits of the
-// float 1.5 * 2^23, so each one reads directly as the float 1.5 * 2^23 + acc
-// (exact: |acc| <= 127 * 127 * 128 < 2^22) and no conversion instruction is
-// needed: p = exp2(t * c - M) with M = m + 1.5 * 2^23 * c rounded once. The
-// rounding of M shifts every exponent of a row by the same amount until the next
-// rescale, and the rescale factor is taken from the M values, so the shift
-// cancels in the normalization. It stays small enough for fp16 (|shift| <=
-// ulp(M) / 2 <= 4) while c < 8; a workgroup with a larger c converts instead.
-constexpr int32_t kBiasBits = 0x4B400000;
-constexpr float kBias = 12582912.0f;
-constexpr float kBiasMaxScale = 8.0f;
 
-template <int D, bool KV_TOKEN, bool PRECISE, bool BIASED>
-__device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
+// SPLIT: the workgroup is two groups of 4 waves over the same 128 query rows;
+// group 0 takes the first half of the key tiles and group 1 the second half, each
+// with its own LDS stages, and group 0 merges both partial results at the end.
+// This halves the longest sequential chain of a workgroup, which balances causal
+// grids that fit the GPU at once.
+template <int D, bool KV_TOKEN, bool PRECISE, bool SPLIT>
+__device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int8_t *smem_all,
                                              float (*sScale)[KV_TOKEN ? 2 * kBN + 1 : 1]) {
+    static_assert(!SPLIT || !KV_TOKEN, "the split kernel has no per-token K/V scales");
     constexpr int KSTRIDE = PrefillLds<D>::KSTRIDE, VSTRIDE = PrefillLds<D>::VSTRIDE;
     constexpr int DB = D / 32;  // 32-wide output blocks
     constexpr int K_BYTES = PrefillLds<D>::K_BYTES, V_BYTES = PrefillLds<D>::V_BYTES;
@@ -151,27 +147,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
     constexpr int VBLOCKS = (kBN / 4) * (D / 8);     // 4-key x 8-channel V blocks
     constexpr float kLazy = 8.0f;  // rescale only when a row max grows by > 2^8
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x & (kThreads - 1), lane = tid & 63;
     // The wave index is the same on every lane; saying so lets every per-wave
     // decision below be a scalar branch instead of predicated vector code.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = SPLIT ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) : 0;
+    int8_t *smem = smem_all + group * PrefillLds<D>::BYTES;
     const int col = lane & 31, grp = lane >> 5;
     int tile, b, h;
-    work_item(a, tile, b, h);
+    item_coords(a, rank, tile, b, h);
     const int kvh = h / (a.q_heads / a.kv_heads);
     const int q0 = tile * kBM;
     const int row = q0 + wave * 32 + col;
     const bool row_ok = row < a.q_len;
-
-    i32x4 qop[D / 32];
-    load_q_operand<D>(qop, a.q + b * a.q_sb + h * a.q_sh + (int64_t)(row_ok ? row : 0) * a.q_st,
-                      row_ok, grp);
-
-    const float cq = row_ok ? scale_of(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
-    const float ck = KV_TOKEN ? 1.0f : scale_of(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-    const float cv = KV_TOKEN ? 1.0f : scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-    // log2-domain score per unit of int32 accumulator
-    const float c = cq * ck * a.score_scale;
 
     // Visible keys of this lane's row: [lo, hi].
     const int pos = a.query_start + row;
@@ -275,10 +263,25 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
         }
     };
 
+    // The first tile, the query operand and the scales are independent loads:
+    // all of them are in flight before anything waits for one.
+    const int kt_first = key_lo / kBN * kBN;
+    const int n_all = (key_hi - kt_first) / kBN + 1;
+    // This group's tiles: [kt0, kt0 + n_tiles * kBN); both groups run n_iter steps.
+    const int n_iter = SPLIT ? (n_all + 1) / 2 : n_all;
+    const int kt0 = kt_first + (group ? n_iter * kBN : 0);
+    const int n_tiles = group ? n_all - n_iter : n_iter;
+    if (n_tiles > 0) load_tile(kt0);
+    i32x4 qop[D / 32];
+    load_q_operand<D>(qop, a.q + b * a.q_sb + h * a.q_sh + (int64_t)(row_ok ? row : 0) * a.q_st,
+                      row_ok, grp);
+    const float cq = row_ok ? scale_of(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
+    const float ck = KV_TOKEN ? 1.0f : scale_of(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    const float cv = KV_TOKEN ? 1.0f : scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    // log2-domain score per unit of int32 accumulator
+    const float c = cq * ck * a.score_scale;
+
     float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
-    // m_run + bias * c, rounded: the offset the biased scores are exponentiated at.
-    const float bias = BIASED ? kBias : 0.0f;
-    float big_run = -INFINITY;
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
@@ -291,8 +294,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
             i32x16 sc[2];
 #pragma unroll
             for (int u = 0; u < 2; ++u)
-                sc[u] = score_tile<D>(qop, sK + (32 * u + col) * KSTRIDE, grp,
-                                      KV_TOKEN ? 0 : kBiasBits);
+                sc[u] = score_tile<D>(qop, sK + (32 * u + col) * KSTRIDE, grp);
 
             // Tile max of the log2-domain scores, masked keys excluded.
             float mt;
@@ -328,7 +330,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
 #pragma unroll
                     for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc[u][r]);
                 // c > 0, so the largest float score is c times the largest integer.
-                mt = mi == INT32_MIN ? -INFINITY : (__int_as_float(mi) - kBias) * c;
+                mt = mi == INT32_MIN ? -INFINITY : (float)mi * c;
             }
             mt = xor32_max(mt);
             float svt = 0.0f;
@@ -350,12 +352,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
                     alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
                     inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
                     s_run = s_new;
-                }
-                if (!KV_TOKEN) {
-                    const float big_new = __builtin_fmaf(bias, c, m_new);
-                    alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(big_run - big_new);
-                    alpha_o = alpha;
-                    big_run = big_new;
                 }
                 m_run = m_new;
                 l_run *= alpha;
@@ -379,9 +375,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
                                 if (x[16 * u + r] == -INFINITY) p = 0.0f;
                             }
                         } else {
-                            const float t = BIASED ? __int_as_float(sc[u][r])
-                                                   : (float)(sc[u][r] - kBiasBits);
-                            p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, c, -big_run));
+                            p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[u][r], c, -m_run));
                             if constexpr (need_mask) {
                                 if (sc[u][r] == INT32_MIN) p = 0.0f;
                             }
@@ -427,16 +421,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
             }
             };
 
-    const int kt0 = key_lo / kBN * kBN;
-    const int n_tiles = (key_hi - kt0) / kBN + 1;
-    load_tile(kt0);
-    store_tile(0);
+    if (n_tiles > 0) store_tile(0);
     __syncthreads();
-    for (int it = 0; it < n_tiles; ++it) {
+    for (int it = 0; it < n_iter; ++it) {
         const int kt = kt0 + it * kBN;
         const int buf = it & 1;
+        const bool mine = it < n_tiles;  // uniform over the group
         if (it + 1 < n_tiles) load_tile(kt + kBN);  // in flight during this tile's math
-        if (wave_active && kt <= wk_hi && kt + kBN - 1 >= wk_lo) {  // wave-uniform
+        if (mine && wave_active && kt <= wk_hi && kt + kBN - 1 >= wk_lo) {  // wave-uniform
             // Tiles inside every row's visible range take the path without masks.
             if (kt + kBN - 1 <= full_hi && kt >= full_lo)
                 tile_math(kt, buf, std::false_type{});
@@ -447,7 +439,37 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
         __syncthreads();
     }
 
-    const float l_tot = xor32_sum(l_run);
+    float l_tot = xor32_sum(l_run);
+    if (SPLIT) {
+        // Group 1 hands (running max, row sum, accumulator) to group 0 through LDS,
+        // in a lane-linear layout (conflict-free 16-byte accesses).
+        f32x4 *xo = reinterpret_cast<f32x4 *>(smem_all);
+        float2 *xml = reinterpret_cast<float2 *>(smem_all + 4 * DB * 4 * kWave * 16);
+        if (group == 1) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    xo[((wave * DB + d) * 4 + j) * kWave + lane] =
+                        f32x4{acc[d][4 * j], acc[d][4 * j + 1], acc[d][4 * j + 2], acc[d][4 * j + 3]};
+            xml[wave * kWave + lane] = float2{m_run, l_tot};
+        }
+        __syncthreads();
+        if (group == 1) return;
+        const float2 other = xml[wave * kWave + lane];
+        const float m = fmaxf(m_run, other.x);
+        const float w0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+        const float w1 = other.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(other.x - m);
+        l_tot = l_tot * w0 + other.y * w1;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 o = xo[((wave * DB + d) * 4 + j) * kWave + lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[d][4 * j + i] = acc[d][4 * j + i] * w0 + o[i] * w1;
+            }
+    }
     if (!row_ok) return;
     const float norm = (KV_TOKEN ? s_run : cv) / l_tot;
     float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
@@ -463,25 +485,34 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int8_t *smem,
     }
 }
 
+// Persistent form of the split kernel: one workgroup per compute unit takes the
+// items of round r = 0, 1, ... at index r * G + blockIdx.x, the odd rounds in
+// reverse order, so that with heaviest-first ranks every workgroup's sum of work
+// is about the same. A workgroup's next item starts while the stores of its last
+// one drain.
+template <int D>
+__global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillArgs a, int items) {
+    static_assert(4 * (D / 32) * 4 * kWave * 16 + 4 * kWave * 8 <= 2 * PrefillLds<D>::BYTES,
+                  "merge buffer fits in the stages");
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * PrefillLds<D>::BYTES];
+    __shared__ float sScale[2][1];
+    const int G = gridDim.x;
+    for (int r = 0;; ++r) {
+        const int item = (r & 1) ? (r + 1) * G - 1 - (int)blockIdx.x : r * G + (int)blockIdx.x;
+        if (item >= items) {
+            if (r * G >= items) break;
+            continue;  // a reversed last round with fewer items than workgroups
+        }
+        prefill_body<D, false, false, true>(a, item, smem, sScale);
+        __syncthreads();  // the next item's stages overwrite the merge buffer
+    }
+}
+
 template <int D, bool KV_TOKEN, bool PRECISE>
 __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
-    bool convert = KV_TOKEN;
-    if (!KV_TOKEN) {
-        // The largest log2-domain score scale of the workgroup's rows.
-        int tile, b, h;
-        work_item(a, tile, b, h);
-        const int kvh = h / (a.q_heads / a.kv_heads);
-        const int row = tile * kBM + (int)threadIdx.x / 2;
-        const float cq = row < a.q_len ? scale_of(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
-        const float ck = scale_of(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-        convert = __syncthreads_or(!(cq * ck * a.score_scale < kBiasMaxScale));
-    }
-    if (convert)
-        prefill_body<D, KV_TOKEN, PRECISE, false>(a, smem, sScale);
-    else
-        prefill_body<D, KV_TOKEN, PRECISE, true>(a, smem, sScale);
+    prefill_body<D, KV_TOKEN, PRECISE, false>(a, grid_rank(a), smem, sScale);
 }
 
 // Bit-exact hook: the int32 score accumulators, through score_tile. One wave
@@ -519,6 +550,15 @@ bool valid_int8_strides(const reef_strides *s, const void *base) {
     if (!s) return true;
     return s->batch >= 0 && s->head >= 0 && s->token >= 0 && s->batch % 16 == 0 &&
            s->head % 16 == 0 && s->token % 16 == 0;
+}
+
+// Compute units of the current device (one split workgroup fits on each).
+int64_t compute_units() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
 }
 
 bool valid_granularity(int32_t g) {
@@ -595,13 +635,34 @@ extern "C" reef_status reef_attention_prefill_int8(
     a.q_tiles = (int32_t)ceil_div(Sq, kBM);
     const int64_t items = a.q_tiles * Hq * p->batch;
     if (items >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
-    // Two workgroups fit on each of the 256 compute units at once.
-    const char *zz = getenv("REEF_PREFILL_ZIGZAG");
-    a.zigzag = zz ? atoi(zz) : (items <= 512 ? 1 : 0);
-
     const dim3 grid((unsigned)items);
     const bool tok = p->kv_granularity == REEF_SCALE_PER_TOKEN;
-    const bool precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0;
+    // Per-token K/V scales fold the value scale into P (p * s_v / max s_v) before its
+    // fp16 rounding, which no longer cancels against the row sum; those launches
+    // always split P into fp16 hi + lo parts to stay well inside the tolerance.
+    const bool precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0 || tok;
+    // With no more items than compute units, the key split of the persistent
+    // kernel is the only parallelism left to balance the causal work; with more,
+    // two one-item workgroups per compute unit overlap each other's prologue and
+    // epilogue better.
+    const char *sp = getenv("REEF_PREFILL_SPLIT");
+    const bool split =
+        !tok && !precise && (sp ? atoi(sp) != 0 : items <= compute_units());
+    // The 4-wave kernel places two workgroups on each of the 256 compute units at
+    // once; zig-zag pairs a heavy and a light tile there. The split kernel holds a
+    // compute unit alone and takes the tiles heaviest first.
+    const char *zz = getenv("REEF_PREFILL_ZIGZAG");
+    a.zigzag = zz ? atoi(zz) : (!split && items <= 512 ? 1 : 0);
+    if (split) {
+        const dim3 pgrid((unsigned)std::min<int64_t>(items, compute_units()));
+        if (D == 128)
+            hipLaunchKernelGGL(prefill_split_kernel<128>, pgrid, dim3(2 * kThreads), 0, stream, a,
+                               (int)items);
+        else
+            hipLaunchKernelGGL(prefill_split_kernel<64>, pgrid, dim3(2 * kThreads), 0, stream, a,
+                               (int)items);
+        return launch_status();
+    }
 #define REEF_PREFILL_LAUNCH(DIM, TOK, PREC)                                                  \
     hipLaunchKernelGGL((prefill_kernel<DIM, TOK, PREC>), grid, dim3(kThreads), 0, stream, a)
     if (D == 128) {

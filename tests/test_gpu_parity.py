@@ -5,6 +5,7 @@ attention outputs must be within max-abs-error 1e-3 of the oracle's golden
 (TOL below) on N(0, 1) data. Each case prints its name before touching the GPU.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -209,11 +210,17 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
     p = oracle.Problem(B, Hq, Hkv, Sq, Skv, D, query_start=start, window=window,
                        softmax_scale=(1 / math.sqrt(D)) if scale is None else scale,
                        q_granularity=gq, kv_granularity=gkv)
-    for precise in (False, True):
-        out, gold = _run_prefill(reef, q, k, v, p, precise)
+    # both fp16 P and split P; the one-item-per-workgroup and the persistent
+    # key-split kernels (chosen by size, forced here through REEF_PREFILL_SPLIT)
+    for precise, split in ((False, "0"), (False, "1"), (True, "0")):
+        os.environ["REEF_PREFILL_SPLIT"] = split
+        try:
+            out, gold = _run_prefill(reef, q, k, v, p, precise)
+        finally:
+            del os.environ["REEF_PREFILL_SPLIT"]
         err = np.abs(out - gold).max()
-        print(f"precise={precise} max_abs_err {err:.3e}", flush=True)
-        assert err <= TOL, (precise, err)
+        print(f"precise={precise} split={split} max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL, (precise, split, err)
 
 
 def test_prefill_rejects_bad_arguments(reef):
