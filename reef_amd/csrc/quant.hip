@@ -47,6 +47,7 @@ __global__ __launch_bounds__(kQuantThreads) void tensor_max(const float *__restr
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int64_t n4 = n / 4;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll 4
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
         const float4 v = x4[i];
         uint32_t a = mag_bits(v.x), b = mag_bits(v.y), c = mag_bits(v.z), d = mag_bits(v.w);
@@ -71,6 +72,7 @@ __global__ __launch_bounds__(kQuantThreads) void tensor_quantize(const float *__
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int64_t n4 = n / 4;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll 4
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
         const float4 v = x4[i];
         bad |= !(__builtin_isfinite(v.x) && __builtin_isfinite(v.y) && __builtin_isfinite(v.z) &&
@@ -96,38 +98,52 @@ __global__ void finalize_scales(float *scales, int64_t n) {
 }
 
 // ---- per head: x [B, H, S, D] with strides; scale per head over (B, S, D) ---------------
+//
+// Block (x, h) walks a contiguous range of the head's B * S rows. A row of D values
+// is VEC ? D / 4 float4 : D floats wide; `tpr` threads share a row (all 256 when a
+// row is wider than the block) and 256 / tpr rows are in flight per step, with
+// 32-bit index arithmetic per row rather than per element.
 
 struct HeadView {
     const float *x;
     int64_t sb, sh, st;  // element strides of batch, head, token
-    int64_t batch, tokens, dim;
+    int32_t batch, tokens, dim;
+    int32_t per_row;        // VEC ? dim / 4 : dim
+    int32_t tpr;            // threads per row: min(per_row rounded up to a power of 2, 256)
+    int32_t rows_per_block;
 };
 
-__device__ __forceinline__ const float *head_row(const HeadView &v, int64_t h, int64_t row) {
-    const int64_t b = row / v.tokens, t = row - b * v.tokens;
+__device__ __forceinline__ const float *head_row(const HeadView &v, int64_t h, int32_t row) {
+    const int32_t b = row / v.tokens, t = row - b * v.tokens;
     return v.x + b * v.sb + h * v.sh + t * v.st;
+}
+
+template <bool VEC>
+__device__ __forceinline__ uint32_t max_of(const float *r, int32_t col) {
+    if (VEC) {
+        const float4 x = reinterpret_cast<const float4 *>(r)[col];
+        uint32_t a = mag_bits(x.x), b = mag_bits(x.y), c = mag_bits(x.z), d = mag_bits(x.w);
+        a = a > b ? a : b;
+        c = c > d ? c : d;
+        return a > c ? a : c;
+    }
+    return mag_bits(r[col]);
 }
 
 template <bool VEC>
 __global__ __launch_bounds__(kQuantThreads) void head_max(HeadView v, uint32_t *max_bits) {
     const int64_t h = blockIdx.y;
-    const int64_t rows = v.batch * v.tokens;
-    const int64_t per_row = VEC ? v.dim / 4 : v.dim;
-    const int64_t total = rows * per_row;
+    const int32_t rows = v.batch * v.tokens;
+    const int32_t r0 = blockIdx.x * v.rows_per_block;
+    const int32_t r1 = min(rows, r0 + v.rows_per_block);
+    const int32_t lane_row = threadIdx.x / v.tpr, lane_col = threadIdx.x % v.tpr;
+    const int32_t step = kQuantThreads / v.tpr;
     uint32_t m = 0;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = i / per_row, col = i - row * per_row;
+#pragma unroll 4
+    for (int32_t row = r0 + lane_row; row < r1; row += step) {
         const float *r = head_row(v, h, row);
-        if (VEC) {
-            const float4 x = reinterpret_cast<const float4 *>(r)[col];
-            uint32_t a = mag_bits(x.x), b = mag_bits(x.y), c = mag_bits(x.z), d = mag_bits(x.w);
-            a = a > b ? a : b;
-            c = c > d ? c : d;
-            a = a > c ? a : c;
-            m = m > a ? m : a;
-        } else {
-            const uint32_t a = mag_bits(r[col]);
+        for (int32_t col = lane_col; col < v.per_row; col += v.tpr) {
+            const uint32_t a = max_of<VEC>(r, col);
             m = m > a ? m : a;
         }
     }
@@ -140,37 +156,93 @@ __global__ __launch_bounds__(kQuantThreads) void head_quantize(HeadView v, const
                                                                uint32_t *status) {
     const int64_t h = blockIdx.y;
     const float scale = int8_scale(__uint_as_float(max_bits[h]));
-    const int64_t rows = v.batch * v.tokens;
-    const int64_t per_row = VEC ? v.dim / 4 : v.dim;
-    const int64_t total = rows * per_row;
+    const int32_t rows = v.batch * v.tokens;
+    const int32_t r0 = blockIdx.x * v.rows_per_block;
+    const int32_t r1 = min(rows, r0 + v.rows_per_block);
+    const int32_t lane_row = threadIdx.x / v.tpr, lane_col = threadIdx.x % v.tpr;
+    const int32_t step = kQuantThreads / v.tpr;
     bool bad = false;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = i / per_row, col = i - row * per_row;
-        const int64_t b = row / v.tokens, t = row - b * v.tokens;
-        const float *r = head_row(v, h, row);
+#pragma unroll 4
+    for (int32_t row = r0 + lane_row; row < r1; row += step) {
+        const int32_t b = row / v.tokens, t = row - b * v.tokens;
+        const float *r = v.x + b * v.sb + h * v.sh + t * v.st;
         int8_t *out = q + ((b * heads + h) * v.tokens + t) * v.dim;
-        if (VEC) {
-            const float4 x = reinterpret_cast<const float4 *>(r)[col];
-            bad |= !(__builtin_isfinite(x.x) && __builtin_isfinite(x.y) &&
-                     __builtin_isfinite(x.z) && __builtin_isfinite(x.w));
-            char4 c;
-            c.x = quantize_int8(x.x, scale);
-            c.y = quantize_int8(x.y, scale);
-            c.z = quantize_int8(x.z, scale);
-            c.w = quantize_int8(x.w, scale);
-            reinterpret_cast<char4 *>(out)[col] = c;
-        } else {
-            bad |= !__builtin_isfinite(r[col]);
-            out[col] = quantize_int8(r[col], scale);
+        for (int32_t col = lane_col; col < v.per_row; col += v.tpr) {
+            if (VEC) {
+                const float4 x = reinterpret_cast<const float4 *>(r)[col];
+                bad |= !(__builtin_isfinite(x.x) && __builtin_isfinite(x.y) &&
+                         __builtin_isfinite(x.z) && __builtin_isfinite(x.w));
+                char4 c;
+                c.x = quantize_int8(x.x, scale);
+                c.y = quantize_int8(x.y, scale);
+                c.z = quantize_int8(x.z, scale);
+                c.w = quantize_int8(x.w, scale);
+                reinterpret_cast<char4 *>(out)[col] = c;
+            } else {
+                bad |= !__builtin_isfinite(r[col]);
+                out[col] = quantize_int8(r[col], scale);
+            }
         }
     }
     if (bad) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
 }
 
-// ---- per token (quantize_rows): one wave per row -----------------------------------------
+// ---- per token (quantize_rows) --------------------------------------------------------------
+//
+// Fast form for rows of at most 256 float4 (width % 4 == 0): LPR lanes per row hold
+// the row's float4 in registers (PER each), so the row is read once; 64 / LPR rows
+// per wave. The largest magnitude is reduced over the LPR lanes of the row.
 
-template <bool VEC>
+template <int LPR, int PER>
+__global__ __launch_bounds__(kQuantThreads) void token_quantize_regs(
+    const float *__restrict__ x, int64_t rows, int32_t w4, int64_t row_stride,
+    int8_t *__restrict__ q, float *__restrict__ scales, uint32_t *status) {
+    constexpr int RPW = kWave / LPR;  // rows per wave
+    const int lane = threadIdx.x % kWave, sub = lane / LPR, l = lane % LPR;
+    const int64_t row =
+        ((int64_t)blockIdx.x * (kQuantThreads / kWave) + threadIdx.x / kWave) * RPW + sub;
+    const bool live = row < rows;
+    const float4 *r = reinterpret_cast<const float4 *>(x + (live ? row : 0) * row_stride);
+    float4 v[PER];
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int col = l + j * LPR;
+        v[j] = (live && col < w4) ? r[col] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t a = mag_bits(v[j].x), b = mag_bits(v[j].y), c = mag_bits(v[j].z),
+                 d = mag_bits(v[j].w);
+        a = a > b ? a : b;
+        c = c > d ? c : d;
+        a = a > c ? a : c;
+        m = m > a ? m : a;
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) {
+        const uint32_t w = (uint32_t)__shfl_xor((int)m, o);
+        m = m > w ? m : w;
+    }
+    const float scale = int8_scale(__uint_as_float(m));
+    if (!live) return;
+    char4 *out = reinterpret_cast<char4 *>(q + row * (int64_t)w4 * 4);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int col = l + j * LPR;
+        if (col < w4) {
+            char4 c;
+            c.x = quantize_int8(v[j].x, scale);
+            c.y = quantize_int8(v[j].y, scale);
+            c.z = quantize_int8(v[j].z, scale);
+            c.w = quantize_int8(v[j].w, scale);
+            out[col] = c;
+        }
+    }
+    if (l == 0) {
+        scales[row] = scale;
+        if (m >= 0x7f800000u) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
+    }
+}
+
+// General form: one wave per row, the row read twice.
 __global__ __launch_bounds__(kQuantThreads) void token_quantize(const float *__restrict__ x,
                                                                 int64_t rows, int64_t width,
                                                                 int64_t row_stride,
@@ -182,50 +254,45 @@ __global__ __launch_bounds__(kQuantThreads) void token_quantize(const float *__r
     if (row >= rows) return;
     const float *r = x + row * row_stride;
     int8_t *out = q + row * width;
-    const int64_t n = VEC ? width / 4 : width;
     uint32_t m = 0;
-    for (int64_t i = lane; i < n; i += kWave) {
-        if (VEC) {
-            const float4 v = reinterpret_cast<const float4 *>(r)[i];
-            uint32_t a = mag_bits(v.x), b = mag_bits(v.y), c = mag_bits(v.z), d = mag_bits(v.w);
-            a = a > b ? a : b;
-            c = c > d ? c : d;
-            a = a > c ? a : c;
-            m = m > a ? m : a;
-        } else {
-            const uint32_t a = mag_bits(r[i]);
-            m = m > a ? m : a;
-        }
+    for (int64_t i = lane; i < width; i += kWave) {
+        const uint32_t a = mag_bits(r[i]);
+        m = m > a ? m : a;
     }
     m = wave_max_u32(m);
     const float scale = int8_scale(__uint_as_float(m));
-    bool bad = m >= 0x7f800000u;
-    for (int64_t i = lane; i < n; i += kWave) {
-        if (VEC) {
-            const float4 v = reinterpret_cast<const float4 *>(r)[i];
-            char4 c;
-            c.x = quantize_int8(v.x, scale);
-            c.y = quantize_int8(v.y, scale);
-            c.z = quantize_int8(v.z, scale);
-            c.w = quantize_int8(v.w, scale);
-            reinterpret_cast<char4 *>(out)[i] = c;
-        } else {
-            out[i] = quantize_int8(r[i], scale);
-        }
-    }
+    for (int64_t i = lane; i < width; i += kWave) out[i] = quantize_int8(r[i], scale);
     if (lane == 0) {
         scales[row] = scale;
-        if (bad) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
+        if (m >= 0x7f800000u) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
     }
 }
 
+// x[i] = float(q[i]) * scales[i / group]. VEC: 4 values per thread (group % 4 == 0,
+// n a whole number of groups); `tpr` threads per group, 256 / tpr groups per step.
+template <bool VEC>
 __global__ __launch_bounds__(kQuantThreads) void dequantize(const int8_t *__restrict__ q, int64_t n,
-                                                            int64_t group,
+                                                            int64_t group, int32_t tpr,
                                                             const float *__restrict__ scales,
                                                             float *__restrict__ x) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        x[i] = (float)q[i] * scales[i / group];
+    const int64_t groups = (n + group - 1) / group;
+    const int64_t per = VEC ? group / 4 : group;
+    const int32_t lane_g = threadIdx.x / tpr, lane_c = threadIdx.x % tpr;
+    const int64_t step = (int64_t)gridDim.x * (kQuantThreads / tpr);
+#pragma unroll 4
+    for (int64_t g = (int64_t)blockIdx.x * (kQuantThreads / tpr) + lane_g; g < groups; g += step) {
+        const float s = scales[g];
+        if (VEC) {
+            const char4 *src = reinterpret_cast<const char4 *>(q + g * group);
+            float4 *dst = reinterpret_cast<float4 *>(x + g * group);
+            for (int64_t c = lane_c; c < per; c += tpr) {
+                const char4 v = src[c];
+                dst[c] = float4{(float)v.x * s, (float)v.y * s, (float)v.z * s, (float)v.w * s};
+            }
+        } else {
+            const int64_t e1 = min(n, (g + 1) * group);
+            for (int64_t i = g * group + lane_c; i < e1; i += tpr) x[i] = (float)q[i] * s;
+        }
     }
 }
 
@@ -247,7 +314,7 @@ extern "C" reef_status reef_quantize_int8_per_tensor(const float *x, int64_t n, 
         return REEF_INVALID_ARGUMENT;
     uint32_t *bits = reinterpret_cast<uint32_t *>(scale);
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, stream, bits, (int64_t)1);
-    const int grid = grid_for(n / 4 + 1);
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(n / 4 + 1, kQuantThreads * 8)));
     hipLaunchKernelGGL(tensor_max, dim3(grid), dim3(kQuantThreads), 0, stream, x, n, bits);
     hipLaunchKernelGGL(tensor_quantize, dim3(grid), dim3(kQuantThreads), 0, stream, x, n,
                        (const uint32_t *)bits, q, status_word);
@@ -263,24 +330,33 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
     if (!x || !q || !scales || batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0 ||
         heads > 65535)
         return REEF_INVALID_ARGUMENT;
+    if (batch * tokens >= (int64_t(1) << 31) || head_dim >= (int64_t(1) << 24))
+        return REEF_UNSUPPORTED;
     HeadView v;
     v.x = x;
     v.sb = xs ? xs->batch : heads * tokens * head_dim;
     v.sh = xs ? xs->head : tokens * head_dim;
     v.st = xs ? xs->token : head_dim;
-    v.batch = batch;
-    v.tokens = tokens;
-    v.dim = head_dim;
+    v.batch = (int32_t)batch;
+    v.tokens = (int32_t)tokens;
+    v.dim = (int32_t)head_dim;
     if (v.sb < 0 || v.sh < 0 || v.st < 0) return REEF_INVALID_ARGUMENT;
     const bool vec = head_dim % 4 == 0 && v.sb % 4 == 0 && v.sh % 4 == 0 && v.st % 4 == 0 &&
                      aligned(x, 16) && aligned(q, 4);
+    v.per_row = (int32_t)(vec ? head_dim / 4 : head_dim);
+    v.tpr = 1;
+    while (v.tpr < v.per_row && v.tpr < kQuantThreads) v.tpr *= 2;
     uint32_t *bits = reinterpret_cast<uint32_t *>(scales);
     hipLaunchKernelGGL(zero_words, dim3((unsigned)ceil_div(heads, 64)), dim3(64), 0, stream, bits,
                        heads);
-    const int64_t per_head = batch * tokens * (vec ? head_dim / 4 : head_dim);
-    // Enough blocks to fill the 256 compute units several times over.
-    const int64_t want = ceil_div(2048, heads);
-    const dim3 grid((unsigned)std::min<int64_t>(want, grid_for(per_head)), (unsigned)heads);
+    // About 1024 blocks in all (4 per compute unit), each a run of whole rows of
+    // at least 8 values per thread.
+    const int64_t rows = batch * tokens;
+    const int64_t rows_min = std::max<int64_t>(1, ceil_div(kQuantThreads * 8, v.per_row));
+    const int64_t blocks_per_head =
+        std::max<int64_t>(1, std::min<int64_t>(ceil_div(1024, heads), ceil_div(rows, rows_min)));
+    v.rows_per_block = (int32_t)ceil_div(rows, blocks_per_head);
+    const dim3 grid((unsigned)ceil_div(rows, v.rows_per_block), (unsigned)heads);
     if (vec) {
         hipLaunchKernelGGL(head_max<true>, grid, dim3(kQuantThreads), 0, stream, v, bits);
         hipLaunchKernelGGL(head_quantize<true>, grid, dim3(kQuantThreads), 0, stream, v,
@@ -301,13 +377,34 @@ extern "C" reef_status reef_quantize_int8_per_token(const float *x, int64_t rows
     if (!x || !q || !scales || rows <= 0 || width <= 0 || row_stride < width)
         return REEF_INVALID_ARGUMENT;
     const bool vec = width % 4 == 0 && row_stride % 4 == 0 && aligned(x, 16) && aligned(q, 4);
-    const dim3 grid((unsigned)ceil_div(rows, kQuantThreads / kWave));
-    if (vec) {
-        hipLaunchKernelGGL(token_quantize<true>, grid, dim3(kQuantThreads), 0, stream, x, rows,
-                           width, row_stride, q, scales, status_word);
+    const int64_t w4 = width / 4;
+    if (vec && w4 <= 4 * kWave) {
+        // lanes per row: the smallest power of two >= w4 (up to 64), then up to 4
+        // float4 per lane
+        int lpr = 1;
+        while (lpr < w4 && lpr < kWave) lpr *= 2;
+        const int rpw = kWave / lpr;
+        const dim3 grid((unsigned)ceil_div(rows, (int64_t)rpw * (kQuantThreads / kWave)));
+#define REEF_TOKEN_LAUNCH(L, P)                                                                \
+    hipLaunchKernelGGL((token_quantize_regs<L, P>), grid, dim3(kQuantThreads), 0, stream, x,   \
+                       rows, (int32_t)w4, row_stride, q, scales, status_word)
+        switch (lpr) {
+        case 1: REEF_TOKEN_LAUNCH(1, 1); break;
+        case 2: REEF_TOKEN_LAUNCH(2, 1); break;
+        case 4: REEF_TOKEN_LAUNCH(4, 1); break;
+        case 8: REEF_TOKEN_LAUNCH(8, 1); break;
+        case 16: REEF_TOKEN_LAUNCH(16, 1); break;
+        case 32: REEF_TOKEN_LAUNCH(32, 1); break;
+        default:
+            if (w4 <= kWave) REEF_TOKEN_LAUNCH(64, 1);
+            else if (w4 <= 2 * kWave) REEF_TOKEN_LAUNCH(64, 2);
+            else REEF_TOKEN_LAUNCH(64, 4);
+        }
+#undef REEF_TOKEN_LAUNCH
     } else {
-        hipLaunchKernelGGL(token_quantize<false>, grid, dim3(kQuantThreads), 0, stream, x, rows,
-                           width, row_stride, q, scales, status_word);
+        const dim3 grid((unsigned)ceil_div(rows, kQuantThreads / kWave));
+        hipLaunchKernelGGL(token_quantize, grid, dim3(kQuantThreads), 0, stream, x, rows, width,
+                           row_stride, q, scales, status_word);
     }
     return launch_status();
 }
@@ -315,8 +412,19 @@ extern "C" reef_status reef_quantize_int8_per_token(const float *x, int64_t rows
 extern "C" reef_status reef_dequantize_int8(const int8_t *q, int64_t n, int64_t group,
                                             const float *scales, float *x, hipStream_t stream) {
     if (!q || !scales || !x || n <= 0 || group <= 0) return REEF_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(dequantize, dim3(grid_for(n)), dim3(kQuantThreads), 0, stream, q, n, group,
-                       scales, x);
+    const bool vec = group % 4 == 0 && n % group == 0 && aligned(q, 4) && aligned(x, 16);
+    const int64_t per = vec ? group / 4 : group;
+    int tpr = 1;
+    while (tpr < per && tpr < kQuantThreads) tpr *= 2;
+    const int64_t groups = ceil_div(n, group);
+    const int64_t blocks =
+        std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(groups, kQuantThreads / tpr)));
+    if (vec)
+        hipLaunchKernelGGL(dequantize<true>, dim3((unsigned)blocks), dim3(kQuantThreads), 0, stream,
+                           q, n, group, tpr, scales, x);
+    else
+        hipLaunchKernelGGL(dequantize<false>, dim3((unsigned)blocks), dim3(kQuantThreads), 0,
+                           stream, q, n, group, tpr, scales, x);
     return launch_status();
 }
 
