@@ -119,7 +119,7 @@ def bench_prefill(torch, reef, W, args):
     return cfg, ops, wall_ms, kern_ms, quant_ms, quant_bytes, (q, k, v, qs, ks, vs)
 
 
-def decode_c3(torch, reef, W, steps, warmup):
+def decode_c3(torch, reef, W, steps, warmup, num_splits=0):
     cfg = W.CONFIGS["c3"]
     g = torch.Generator(device="cuda")
     g.manual_seed(cfg.seed)
@@ -136,18 +136,18 @@ def decode_c3(torch, reef, W, steps, warmup):
     del vq
     out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
     status = reef.StatusWord()
-    p = reef._decode_params(q, L, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN, 0)
+    p = reef._decode_params(q, L, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN, num_splits)
     ws = reef.decode_workspace(p, q.device)
 
     def launch():
         reef.attention_decode(q, qsc, k, vp, ksc, vsc, None, softmax_scale=1 / math.sqrt(D),
-                              workspace=ws, status=status, out=out)
+                              num_splits=num_splits, workspace=ws, status=status, out=out)
     wall_ms, kern_ms = timed(torch, launch, steps, warmup)
     status.check("decode")
     return cfg, cfg.kv_bytes(), wall_ms, kern_ms
 
 
-def decode_c5b(torch, reef, W, steps, warmup, pools=3):
+def decode_c5b(torch, reef, W, steps, warmup, pools=3, num_splits=0):
     """Ragged paged decode. The pages of one step (about 150 MB) fit in the 256 MB
     last-level cache, so steps rotate over `pools` independent page pools."""
     cfg = W.CONFIGS["c5b"]
@@ -181,7 +181,8 @@ def decode_c5b(torch, reef, W, steps, warmup, pools=3):
     lens_t = torch.from_numpy(lens.astype(np.int32)).cuda()
     out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
     status = reef.StatusWord()
-    p = reef._decode_params(q, max_blocks * 16, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN, 0)
+    p = reef._decode_params(q, max_blocks * 16, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN,
+                            num_splits)
     ws = reef.decode_workspace(p, q.device)
     it = [0]
 
@@ -189,8 +190,8 @@ def decode_c5b(torch, reef, W, steps, warmup, pools=3):
         kp, vp, ksp, vsp, table = setups[it[0] % pools]
         it[0] += 1
         reef.attention_decode_paged(q, qsc, kp, vp, ksp, vsp, table, lens_t,
-                                    softmax_scale=1 / math.sqrt(D), workspace=ws,
-                                    status=status, out=out)
+                                    softmax_scale=1 / math.sqrt(D), num_splits=num_splits,
+                                    workspace=ws, status=status, out=out)
     wall_ms, kern_ms = timed(torch, launch, steps, warmup)
     status.check("decode paged")
     return cfg, cfg.kv_bytes(lens), wall_ms, kern_ms

@@ -45,7 +45,7 @@ struct DecodeArgs {
     float *part_ml;         // [B, Hq, splits, 2] (max in log2 units, sum)
     uint32_t *status;
     int32_t batch, q_heads, kv_heads, group;
-    int32_t max_context, window, splits, chunk;  // chunk: keys per split, multiple of 64
+    int32_t max_context, window, splits;
     int32_t max_blocks, num_pages;               // paged only
     int32_t q_gran;
     float score_scale;  // softmax_scale * log2(e)
@@ -91,17 +91,36 @@ __device__ __forceinline__ PageRef page_ref(const DecodeArgs &a, int b, int kvh,
     return r;
 }
 
-// int8 x 16 (one 16-byte word) -> two fp16 x 8 operands, exactly.
+// int8 x 16 (one 16-byte word) -> two fp16 x 8 operands, exactly. After the XOR a
+// byte holds u = b + 128; a byte permute puts each u under the exponent byte 0x64,
+// which reads as the fp16 1024 + u, and subtracting 1152 leaves b. Five
+// instructions per 4 values.
 __device__ __forceinline__ void int8x16_to_f16(i32x4 w, f16x8 &lo, f16x8 &hi) {
+    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        lo[e] = (_Float16)(int)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
-        hi[e] = (_Float16)(int)(int8_t)(w[2 + (e >> 2)] >> (8 * (e & 3)));
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t u = (uint32_t)w[j] ^ 0x80808080u;
+        const f16x2 a = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+        const f16x2 c = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+        f16x8 &dst = j < 2 ? lo : hi;
+        const int e = 4 * (j & 1);
+        dst[e] = a[0];
+        dst[e + 1] = a[1];
+        dst[e + 2] = c[0];
+        dst[e + 3] = c[1];
     }
 }
 
+// A 16-byte load of the streamed cache; NT marks it non-temporal (read once: a
+// contiguous cache is not re-read within a step, and keeping it out of the caches
+// measured faster there).
+template <bool NT>
+__device__ __forceinline__ i32x4 load_stream(const i32x4 *p) {
+    return NT ? __builtin_nontemporal_load(p) : *p;
+}
+
 template <int D, bool PAGED>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs a) {
     constexpr int KS = D / 64;   // 64-wide reduction steps of the score instruction
     constexpr int DB = D / 16;   // 16-wide output blocks
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -119,9 +138,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
         len = 0;
     }
     const int lo = a.window > 0 ? max(0, len - a.window) : 0;
-    const int k_begin = max(split * a.chunk, lo / kBlockKeys * kBlockKeys);
-    const int k_end = min((split + 1) * a.chunk, len);
+    // Split s takes the 64-key blocks first + s, first + s + splits, ...: at any
+    // moment the splits of a sequence read neighbouring blocks, which keeps the
+    // DRAM accesses of the waves running together close.
+    const int k_step = a.splits * kBlockKeys;
+    const int k_begin = (lo / kBlockKeys + split) * kBlockKeys;
+    const int k_end = len;
     const int n_pages = (len + kPage - 1) / kPage;
+    // A split with no keys of this sequence writes nothing; the combine skips it.
+    if (k_begin >= k_end) return;
 
     // q^T operand: 16 bytes of head `head` per 64-wide reduction step.
     i32x4 qop[KS];
@@ -138,13 +163,23 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
     }
     const float c = cq * a.score_scale;
 
-    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
     f32x4 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x4{};
     bool bad_page = false;
 
-    for (int kb = k_begin; kb < k_end; kb += kBlockKeys) {
+    // One 64-key block in registers: the operands of both matrix products and,
+    // per lane, the K and V scale of key 16 grp + col (the 16 lanes of a group
+    // hold the 16 scales of its page, handed around with shuffles). The next
+    // block's loads are issued before the current block is computed.
+    struct Block {
+        i32x4 k[4][KS];
+        i32x4 v[DB];
+        float ks, vs;
+        bool live;
+    };
+    auto load_block = [&](int kb, Block &x) {
         const int page0 = kb / kPage;
         // K rows for the score instruction: row m = col of block t is key
         // 16 (m / 4) + 4t + (m % 4), in page m / 4.
@@ -152,24 +187,35 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
         // This lane group's page for scales, P and V.
         const PageRef gp = page_ref<D, PAGED>(a, b, kvh, page0 + grp, n_pages);
         bad_page |= !gp.ok;
-
-        i32x4 kop[4][KS];
+        x.live = gp.live;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int s = 0; s < KS; ++s)
-                kop[t][s] = *reinterpret_cast<const i32x4 *>(kp.k + (4 * t + (col & 3)) * D +
-                                                             64 * s + 16 * grp);
-        i32x4 vop[DB];
+                x.k[t][s] = load_stream<!PAGED>(reinterpret_cast<const i32x4 *>(
+                    kp.k + (4 * t + (col & 3)) * D + 64 * s + 16 * grp));
 #pragma unroll
         for (int d = 0; d < DB; ++d)
-            vop[d] = *reinterpret_cast<const i32x4 *>(gp.vt + (16 * d + col) * kPage);
-        f32x4 ksc[4], vsc[4];
+            x.v[d] = load_stream<!PAGED>(
+                reinterpret_cast<const i32x4 *>(gp.vt + (16 * d + col) * kPage));
+        x.ks = gp.ks[col];
+        x.vs = gp.vs[col];
+    };
+    Block cur, nxt;
+    if (k_begin < k_end) load_block(k_begin, cur);
+    for (int kb = k_begin; kb < k_end; kb += k_step) {
+        const bool more = kb + k_step < k_end;
+        if (more) load_block(kb + k_step, nxt);
+        const auto &kop = cur.k;
+        const auto &vop = cur.v;
+        const int row0 = lane & ~15;  // first lane of this lane group
+        float ksc[16], vsc[16];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            ksc[t] = *reinterpret_cast<const f32x4 *>(gp.ks + 4 * t);
-            vsc[t] = *reinterpret_cast<const f32x4 *>(gp.vs + 4 * t);
+        for (int r = 0; r < 16; ++r) {
+            ksc[r] = __shfl(cur.ks, row0 + r);
+            vsc[r] = __shfl(cur.vs, row0 + r);
         }
+        const bool live_g = cur.live;
 
         float x[16];
 #pragma unroll
@@ -178,51 +224,65 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) s = mfma_16x16x64_i8(kop[t][ks], qop[ks], s);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[4 * t + i] = (float)s[i] * (c * ksc[t][i]);
+            for (int i = 0; i < 4; ++i) x[4 * t + i] = (float)s[i] * (c * ksc[4 * t + i]);
         }
-        // Keys outside [lo, k_end) or on a dead page take no part: score -inf and
+        // Blocks wholly inside [lo, k_end) on live pages skip the masks. In the
+        // others, keys outside or on a dead page take no part: score -inf and
         // value scale 0 (the cache past a sequence's end may hold anything).
+        const bool full = kb >= lo && kb + kBlockKeys <= k_end && __all(live_g);
         float vv[16];
+        if (full) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kb + 16 * grp + r;
-            const bool vis = key >= lo && key < k_end && gp.live;
-            if (!vis) x[r] = -INFINITY;
-            vv[r] = vis ? vsc[r >> 2][r & 3] : 0.0f;
+            for (int r = 0; r < 16; ++r) vv[r] = vsc[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kb + 16 * grp + r;
+                const bool vis = key >= lo && key < k_end && live_g;
+                if (!vis) x[r] = -INFINITY;
+                vv[r] = vis ? vsc[r] : 0.0f;
+            }
         }
-        float mt = x[0], vmax = vv[0];
+        float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        float vmax = fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3]));
 #pragma unroll
-        for (int r = 1; r < 16; ++r) {
-            mt = fmaxf(mt, x[r]);
-            vmax = fmaxf(vmax, vv[r]);
+        for (int r = 4; r < 16; r += 2) {
+            mt = fmaxf(mt, fmaxf(x[r], x[r + 1]));
+            vmax = fmaxf(vmax, fmaxf(vv[r], vv[r + 1]));
         }
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
         vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
 
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        // Values accumulate in units of s_run, the largest value scale so far,
-        // so p * v_scale / s_run stays within [0, 1] in fp16.
-        const float s_new = fmaxf(s_run, vmax);
-        const float alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
-        const float inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
-        m_run = m_new;
-        s_run = s_new;
-        l_run *= alpha;
+        // Lazy rescale: the running max moves only when a head's block max exceeds
+        // it by more than 2^8, and the value normalizer s_run (values accumulate in
+        // units of s_run, the largest value scale so far) only when a value scale
+        // exceeds it 16-fold, so p * v_scale / s_run stays below 2^12 in fp16.
+        if (__any(mt > m_run + 8.0f || vmax > s_run * 16.0f)) {
+            const float m_new = fmaxf(m_run, mt);
+            const float s_new = fmaxf(s_run, vmax);
+            const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            const float alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
+            inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
+            m_run = m_new;
+            s_run = s_new;
+            l_run *= alpha;
 #pragma unroll
-        for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
+            for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
 
         // P operand: lane group g's keys 16g + 8h + e for the two halves h.
         f16x8 pop[2];
+        float lp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const float p = __builtin_amdgcn_exp2f(x[r] - m_use);
-            l_run += p;
+            lp[r & 3] += p;
             pop[r >> 3][r & 7] = (_Float16)(p * (vv[r] * inv_s));
         }
+        l_run += (lp[0] + lp[1]) + (lp[2] + lp[3]);
         // out^T = V^T . P^T: the output column is the head (lane % 16), the lane
         // that owns the head's running max, so the rescale above is per lane.
 #pragma unroll
@@ -232,6 +292,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
             acc[d] = mfma_16x16x32_f16(v0, pop[0], acc[d]);
             acc[d] = mfma_16x16x32_f16(v1, pop[1], acc[d]);
         }
+        if (more) cur = nxt;
     }
     if (bad_page) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
 
@@ -253,28 +314,49 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_kernel(DecodeArgs a)
     }
 }
 
-// out[b, h, :] = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s.
+// out[b, h, :] = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s, over
+// the splits that hold keys of sequence b (the others wrote nothing). One wave per
+// (b, h): lane s reads split s's (m, l); the output loop's loads are independent.
 template <int D>
 __global__ __launch_bounds__(64) void decode_combine(const float *__restrict__ part_o,
                                                      const float *__restrict__ part_ml,
-                                                     int32_t splits, float *__restrict__ out) {
+                                                     DecodeArgs a, float *__restrict__ out) {
     const int64_t bh = blockIdx.x;
     const int lane = threadIdx.x;
+    const int splits = a.splits;
+    const int b = (int)(bh / a.q_heads);
+    int len = a.context_lens ? a.context_lens[b] : a.max_context;
+    if (len < 1 || len > a.max_context) len = 0;
+    const int lo = a.window > 0 ? max(0, len - a.window) : 0;
+    // split s is live when block lo / 64 + s starts before len
+    const int live = len > 0 ? min(splits, (len + kBlockKeys - 1) / kBlockKeys - lo / kBlockKeys) : 0;
     const float *ml = part_ml + bh * splits * 2;
-    float m = -INFINITY;
-    for (int s = 0; s < splits; ++s) m = fmaxf(m, ml[2 * s]);
-    const float m_use = m == -INFINITY ? 0.0f : m;
-    float l = 0.0f;
+    const float *po = part_o + bh * splits * D;
     float o[D / 64];
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) o[j] = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-        const float w = __builtin_amdgcn_exp2f(ml[2 * s] - m_use);
-        l += ml[2 * s + 1] * w;
-        const float *po = part_o + (bh * splits + s) * D;
-#pragma unroll
-        for (int j = 0; j < D / 64; ++j) o[j] += po[64 * j + lane] * w;
+    float l = 0.0f;
+    // splits beyond 64 are folded in chunks of 64 lanes
+    float m = -INFINITY;
+    for (int s0 = 0; s0 < live; s0 += kWave) {
+        const int s = s0 + lane;
+        m = fmaxf(m, s < live ? ml[2 * s] : -INFINITY);
     }
+    m = wave_max(m);
+    const float m_use = m == -INFINITY ? 0.0f : m;
+    for (int s0 = 0; s0 < live; s0 += kWave) {
+        const int s = s0 + lane;
+        const float w = s < live ? __builtin_amdgcn_exp2f(ml[2 * s] - m_use) : 0.0f;
+        l += s < live ? w * ml[2 * s + 1] : 0.0f;
+        const int n = min(kWave, live - s0);
+#pragma unroll 4
+        for (int i = 0; i < n; ++i) {
+            const float wi = __shfl(w, i);
+#pragma unroll
+            for (int j = 0; j < D / 64; ++j) o[j] += po[(int64_t)(s0 + i) * D + 64 * j + lane] * wi;
+        }
+    }
+    l = wave_sum(l);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) out[bh * D + 64 * j + lane] = o[j] * inv;
@@ -329,7 +411,6 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
                           hipStream_t stream) {
     const int splits = default_splits(p);
     a.splits = splits;
-    a.chunk = (int32_t)(ceil_div(ceil_div(p->max_context, splits), kBlockKeys) * kBlockKeys);
     a.batch = (int32_t)p->batch;
     a.q_heads = (int32_t)p->q_heads;
     a.kv_heads = (int32_t)p->kv_heads;
@@ -346,11 +427,11 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
         hipLaunchKernelGGL((decode_kernel<64, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
     const dim3 cgrid((unsigned)(p->batch * p->q_heads));
     if (p->head_dim == 128)
-        hipLaunchKernelGGL(decode_combine<128>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml,
-                           splits, out);
+        hipLaunchKernelGGL(decode_combine<128>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml, a,
+                           out);
     else
-        hipLaunchKernelGGL(decode_combine<64>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml,
-                           splits, out);
+        hipLaunchKernelGGL(decode_combine<64>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml, a,
+                           out);
     return launch_status();
 }
 
