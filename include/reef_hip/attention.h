@@ -145,6 +145,22 @@ reef_status reef_qk_scores_i32(const int8_t *q, const int8_t *k, int64_t batch, 
                                int64_t kv_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,
                                int32_t *acc, hipStream_t stream);
 
+/* Integer-only attention: attend_head_int8 (int8.hpp:250-279) for every (batch,
+ * head) in one launch, bit-identical to the engine. Per row: int32 scores over the
+ * visible keys, weights table[min((max - s) >> score_shift, 255)], probabilities
+ * in [0, 255] from the integer reciprocal of their sum (masked_softmax_int8,
+ * :180-232), out = saturate_int8(rounding_shift(sum p * v, out_shift)) (:43-60).
+ * table: 256 uint16 on the device (exp_table(), :156-164). q, k, v int8
+ * [B, H, S, D] with strides as for the prefill; out int8 [B, Hq, q_len, D].
+ * p->softmax_scale, q_granularity, kv_granularity and flags are not used;
+ * head_dim 32, 64 or 128; score_shift and out_shift at most 31. */
+reef_status reef_attention_int8_integer(const reef_attention_params *p, const int8_t *q,
+                                        const reef_strides *q_strides, const int8_t *k,
+                                        const reef_strides *k_strides, const int8_t *v,
+                                        const reef_strides *v_strides, uint32_t score_shift,
+                                        const uint16_t *table, uint32_t out_shift, int8_t *out,
+                                        const reef_strides *out_strides, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Decode over an int8 KV cache (one query token per sequence), split across
  * workgroups along the keys, partial results combined by log-sum-exp.

@@ -32,7 +32,7 @@ EXPORTS = [
     "reef_attention_prefill_int8", "reef_qk_scores_i32",
     "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
     "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages", "reef_kv_append_int8",
-    "reef_kv_append_int8_paged",
+    "reef_kv_append_int8_paged", "reef_attention_int8_integer",
 ]
 
 
@@ -107,6 +107,9 @@ _SIGS = {
     "reef_attention_decode_int8_paged": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P,
                                          _I64, _I64, _P, _P, _P, C.c_size_t, _P, _P],
     "reef_kv_pack_v_pages": [_P, _I64, _I64, _P, _P],
+    "reef_attention_int8_integer": [C.POINTER(AttentionParams), _P, C.POINTER(Strides), _P,
+                                    C.POINTER(Strides), _P, C.POINTER(Strides), C.c_uint32, _P,
+                                    C.c_uint32, _P, C.POINTER(Strides), _P],
     "reef_kv_append_int8": [C.POINTER(KvAppendParams), _P, C.POINTER(Strides), _P,
                             C.POINTER(Strides), _P, _P, _P, _P, _P, _P, _P, _P],
     "reef_kv_append_int8_paged": [C.POINTER(KvAppendParams), _P, C.POINTER(Strides), _P,
@@ -441,3 +444,28 @@ def kv_append_paged(k_new, v_new, start_positions, block_table, k_pages, v_pages
         "kv_append_paged")
     if status is None:
         own.check("kv_append_paged")
+
+
+# --- integer-only attention (int8.hpp:156-279) -----------------------------------------
+
+def attention_int8_integer(q, k, v, table, *, score_shift, out_shift=8, query_start=None,
+                           window=0):
+    """attend_head_int8 for every (batch, head): q [B, Hq, Sq, D], k and v
+    [B, Hkv, Skv, D] int8, table [256] uint16 (as int16/uint16 torch tensor) on the
+    device; returns int8 [B, Hq, Sq, D], bit-identical to the engine."""
+    torch = _torch()
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t, torch.int8, n)
+    if table.numel() != 256 or table.element_size() != 2 or not table.is_cuda:
+        raise InvalidArgument("table must hold 256 16-bit entries on the GPU")
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    start = Skv - Sq if query_start is None else query_start
+    p = AttentionParams(B, Hq, Hkv, Sq, Skv, D, start, window, 1.0, PER_HEAD, PER_HEAD, 0)
+    out = torch.empty((B, Hq, Sq, D), dtype=torch.int8, device=q.device)
+    sq, sk, sv, so = _strides4(q), _strides4(k), _strides4(v), _strides4(out)
+    check(lib().reef_attention_int8_integer(
+        C.byref(p), _ptr(q), C.byref(sq), _ptr(k), C.byref(sk), _ptr(v), C.byref(sv),
+        score_shift, _ptr(table.contiguous()), out_shift, _ptr(out), C.byref(so), _stream()),
+        "attention_int8_integer")
+    return out

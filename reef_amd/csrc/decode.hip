@@ -381,9 +381,9 @@ int default_splits(const reef_decode_params *p) {
     if (p->num_splits > 0) return p->num_splits;
     const int64_t blocks = ceil_div(p->max_context, kBlockKeys);
     const int64_t pairs = p->batch * p->kv_heads;
-    // Aim for about 4096 waves over the 256 compute units, at least 4 blocks
-    // (256 keys) per split.
-    int64_t s = ceil_div(4096, pairs);
+    // Aim for about 2048 waves (8 per compute unit, all resident at once), at
+    // least 4 blocks (256 keys) per split.
+    int64_t s = ceil_div(2048, pairs);
     s = std::min<int64_t>(s, ceil_div(blocks, 4));
     return (int)std::max<int64_t>(1, s);
 }

@@ -1,0 +1,288 @@
+// Integer-only int8 attention for gfx950: the engine's attend_head_int8
+// (int8.hpp:250-279) for every (batch, head) in one launch, bit-exact.
+//
+// Per query row (int8.hpp:180-232): int32 scores s = q . k over the visible keys,
+// d = (max - s) >> score_shift, weight w = table[min(d, 255)], reciprocal
+// r = (255 << 16) / sum(w), probability p = min(round_half_up(w * r / 2^16), 255),
+// then out = saturate_int8(rounding_shift(sum_k p * v, out_shift)) (:43-60).
+//
+// The weights depend on the row's final maximum and the probabilities on the
+// final sum, so the keys are visited three times (maximum, sum, output), each
+// time recomputing the exact int32 scores on v_mfma_i32_32x32x32_i8 rather than
+// storing them. p * v runs on v_mfma_f32_32x32x16_f16: p <= 255 and v are exact
+// in fp16, and every partial sum is an integer below 2^24 (at most 510 keys can
+// carry p > 0 beyond the ~255 the probabilities sum to, so |sum| <= 128 * 510),
+// so the fp32 accumulation is exact and the result is the engine's integer.
+#include <algorithm>
+
+#include "reef_common.hpp"
+
+namespace reef {
+namespace {
+
+constexpr int kIntThreads = 256;  // 4 waves x 32 query rows
+constexpr int kIntRows = 128;
+constexpr int kIntKeys = 64;  // keys per tile
+
+struct IntHeadArgs {
+    const int8_t *q, *k, *v;
+    const uint16_t *table;
+    int8_t *out;
+    int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
+    int32_t batch, q_heads, kv_heads, q_len, kv_len, query_start, window;
+    int32_t score_shift, out_shift, q_tiles;
+};
+
+// Row m of a 32-key score block holds key 16 ((m >> 2) & 1) + 4 (m >> 3) + (m & 3),
+// so that output register r of lane group g is key 16 g + r.
+__device__ __forceinline__ int int_key_of_row(int m) {
+    return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
+}
+
+// Scores of a 32-key block for this lane's query: register r of lane group g is
+// key kb + 16 g + r. Keys past kv_len read key 0 (their scores are masked).
+template <int D>
+__device__ __forceinline__ i32x16 int_scores(const i32x4 (&qop)[D / 32], const int8_t *kbase,
+                                             int64_t k_st, int kb, int kv_len, int col, int grp) {
+    const int key = kb + int_key_of_row(col);
+    const int8_t *krow = kbase + (int64_t)(key < kv_len ? key : 0) * k_st;
+    i32x16 s = {};
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) {
+        const i32x4 kop = *reinterpret_cast<const i32x4 *>(krow + 32 * t + 16 * grp);
+        s = mfma_32x32x32_i8(kop, qop[t], s);
+    }
+    return s;
+}
+
+__device__ __forceinline__ int32_t rounding_shift_dev(int32_t value, int shift) {
+    return shift == 0 ? value : (value >> shift) + ((value >> (shift - 1)) & 1);
+}
+
+template <int D>
+__global__ __launch_bounds__(kIntThreads) void int_head_kernel(IntHeadArgs a) {
+    constexpr int DB = D / 32;
+    __shared__ uint16_t sTable[256];
+    __shared__ __attribute__((aligned(16))) int8_t sV[kIntKeys * D];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, grp = lane >> 5;
+    sTable[tid] = a.table[tid];  // 256 threads, 256 entries
+
+    const int pairs = a.batch * a.q_heads;
+    const int tile = a.q_tiles - 1 - (int)blockIdx.x / pairs;  // heaviest first
+    const int bh = (int)blockIdx.x % pairs;
+    const int b = bh / a.q_heads, h = bh % a.q_heads;
+    const int kvh = h / (a.q_heads / a.kv_heads);
+    const int q0 = tile * kIntRows;
+    const int row = q0 + wave * 32 + col;
+    const bool row_ok = row < a.q_len;
+
+    i32x4 qop[DB];
+    const int8_t *qrow = a.q + b * a.q_sb + h * a.q_sh + (int64_t)(row_ok ? row : 0) * a.q_st;
+#pragma unroll
+    for (int t = 0; t < DB; ++t)
+        qop[t] = row_ok ? *reinterpret_cast<const i32x4 *>(qrow + 32 * t + 16 * grp)
+                        : i32x4{0, 0, 0, 0};
+
+    // Visible keys: of this lane's row [lo, hi], of the wave, of the workgroup.
+    const int pos = a.query_start + row;
+    const int lo = a.window > 0 ? max(0, pos + 1 - a.window) : 0;
+    const int hi = min(pos, a.kv_len - 1);
+    const int w_first = q0 + wave * 32;
+    const int w_last = min(w_first + 31, a.q_len - 1);
+    const bool wave_active = w_first < a.q_len;
+    const int wk_lo = a.window > 0 ? max(0, a.query_start + w_first + 1 - a.window) : 0;
+    const int wk_hi = min(a.query_start + w_last, a.kv_len - 1);
+    const int r_last = min(q0 + kIntRows, a.q_len) - 1;
+    const int key_lo = a.window > 0 ? max(0, a.query_start + q0 + 1 - a.window) : 0;
+    const int key_hi = min(a.query_start + r_last, a.kv_len - 1);
+    const int kt0 = key_lo / kIntKeys * kIntKeys;
+
+    const int8_t *kbase = a.k + b * a.k_sb + kvh * a.k_sh;
+    const int8_t *vbase = a.v + b * a.v_sb + kvh * a.v_sh;
+    __syncthreads();  // the table
+
+    auto visible = [&](int key) { return key >= lo && key <= hi; };
+    auto wave_needs = [&](int kt) { return wave_active && kt <= wk_hi && kt + kIntKeys - 1 >= wk_lo; };
+
+    // Pass 1: the row maximum over visible keys (int8.hpp:197-203).
+    int32_t mx = INT32_MIN;
+    for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
+        if (!wave_needs(kt)) continue;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const i32x16 s = int_scores<D>(qop, kbase, a.k_st, kt + 32 * u, a.kv_len, col, grp);
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (visible(kt + 32 * u + 16 * grp + r)) mx = max(mx, s[r]);
+        }
+    }
+    {
+        const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)mx, (uint32_t)mx, false, false);
+        mx = max((int32_t)sw[0], (int32_t)sw[1]);
+    }
+
+    // Pass 2: the sum of table weights (:208-217).
+    uint32_t sum = 0;
+    for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
+        if (!wave_needs(kt)) continue;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const i32x16 s = int_scores<D>(qop, kbase, a.k_st, kt + 32 * u, a.kv_len, col, grp);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (visible(kt + 32 * u + 16 * grp + r)) {
+                    const uint32_t d = (uint32_t)((mx - s[r]) >> a.score_shift);
+                    sum += sTable[d < 255u ? d : 255u];
+                }
+            }
+        }
+    }
+    {
+        const auto sw = __builtin_amdgcn_permlane32_swap(sum, sum, false, false);
+        sum = sw[0] + sw[1];
+    }
+    // The maximum's weight is the table's first entry, so sum > 0 on a row that
+    // sees a key; rows outside the tensor never store.
+    const uint32_t recip = sum > 0 ? (255u << 16) / sum : 0u;
+
+    // Pass 3: probabilities and P.V (:218-227, 268-276). The value tile is staged
+    // token-major in LDS; each lane gathers its 8 keys of one channel.
+    f32x16 acc[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
+    for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
+        __syncthreads();  // the previous tile's readers are done
+        for (int i = tid; i < kIntKeys * D / 16; i += kIntThreads) {
+            const int key = kt + i / (D / 16), c16 = i % (D / 16);
+            i32x4 w = {0, 0, 0, 0};
+            if (key < a.kv_len)
+                w = *reinterpret_cast<const i32x4 *>(vbase + (int64_t)key * a.v_st + 16 * c16);
+            *reinterpret_cast<i32x4 *>(sV + (key - kt) * D + 16 * c16) = w;
+        }
+        __syncthreads();
+        if (!wave_needs(kt)) continue;
+        f16x8 pop[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const i32x16 s = int_scores<D>(qop, kbase, a.k_st, kt + 32 * u, a.kv_len, col, grp);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                uint32_t p = 0;
+                if (visible(kt + 32 * u + 16 * grp + r)) {
+                    const uint32_t d = (uint32_t)((mx - s[r]) >> a.score_shift);
+                    const uint32_t scaled = (uint32_t)sTable[d < 255u ? d : 255u] * recip;
+                    p = (scaled >> 16) + ((scaled >> 15) & 1u);
+                    p = p < 255u ? p : 255u;
+                }
+                pop[u][r >> 3][r & 7] = (_Float16)(float)p;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int s8 = 0; s8 < 2; ++s8) {
+                const int k0 = 32 * u + 16 * grp + 8 * s8;  // this lane's 8 keys in the tile
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+                    f16x8 vop;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) vop[e] = (_Float16)(float)sV[(k0 + e) * D + 32 * d + col];
+                    acc[d] = mfma_32x32x16_f16(vop, pop[u][s8], acc[d]);
+                }
+            }
+    }
+
+    if (!row_ok) return;
+    // acc[d][4j + i] is channel 32 d + 8 j + 4 grp + i of this lane's row.
+    int8_t *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            char4 c4;
+            int8_t *cp = reinterpret_cast<int8_t *>(&c4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int32_t sum_pv = (int32_t)acc[d][4 * j + i];
+                const int32_t sh = rounding_shift_dev(sum_pv, a.out_shift);
+                cp[i] = (int8_t)(sh < -128 ? -128 : (sh > 127 ? 127 : sh));
+            }
+            *reinterpret_cast<char4 *>(orow + 32 * d + 8 * j + 4 * grp) = c4;
+        }
+}
+
+bool int8_strides_ok(const reef_strides *s, const void *base) {
+    if (!aligned(base, 16)) return false;
+    if (!s) return true;
+    return s->batch >= 0 && s->head >= 0 && s->token >= 0 && s->batch % 16 == 0 &&
+           s->head % 16 == 0 && s->token % 16 == 0;
+}
+
+}  // namespace
+}  // namespace reef
+
+using namespace reef;
+
+extern "C" reef_status reef_attention_int8_integer(
+    const reef_attention_params *p, const int8_t *q, const reef_strides *q_strides,
+    const int8_t *k, const reef_strides *k_strides, const int8_t *v,
+    const reef_strides *v_strides, uint32_t score_shift, const uint16_t *table,
+    uint32_t out_shift, int8_t *out, const reef_strides *out_strides, hipStream_t stream) {
+    if (!p || !q || !k || !v || !table || !out) return REEF_INVALID_ARGUMENT;
+    const int64_t D = p->head_dim;
+    if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->q_len <= 0 ||
+        p->kv_len <= 0 || D <= 0 || p->q_heads % p->kv_heads != 0 || p->query_start < 0 ||
+        p->window < 0 || p->query_start + p->q_len > p->kv_len || score_shift > 31 ||
+        out_shift > 31)
+        return REEF_INVALID_ARGUMENT;
+    if (D != 32 && D != 64 && D != 128) return REEF_UNSUPPORTED;
+    if (p->kv_len >= (int64_t(1) << 30) || p->window >= (int64_t(1) << 30)) return REEF_UNSUPPORTED;
+    if (!int8_strides_ok(q_strides, q) || !int8_strides_ok(k_strides, k) ||
+        !int8_strides_ok(v_strides, v) || !aligned(out, 4))
+        return REEF_INVALID_ARGUMENT;
+    if (out_strides && (out_strides->batch % 4 || out_strides->head % 4 || out_strides->token % 4 ||
+                        out_strides->batch < 0 || out_strides->head < 0 || out_strides->token < 0))
+        return REEF_INVALID_ARGUMENT;
+    IntHeadArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.table = table;
+    a.out = out;
+    const int64_t Hq = p->q_heads, Hkv = p->kv_heads, Sq = p->q_len, Skv = p->kv_len;
+    a.q_sb = q_strides ? q_strides->batch : Hq * Sq * D;
+    a.q_sh = q_strides ? q_strides->head : Sq * D;
+    a.q_st = q_strides ? q_strides->token : D;
+    a.k_sb = k_strides ? k_strides->batch : Hkv * Skv * D;
+    a.k_sh = k_strides ? k_strides->head : Skv * D;
+    a.k_st = k_strides ? k_strides->token : D;
+    a.v_sb = v_strides ? v_strides->batch : Hkv * Skv * D;
+    a.v_sh = v_strides ? v_strides->head : Skv * D;
+    a.v_st = v_strides ? v_strides->token : D;
+    a.o_sb = out_strides ? out_strides->batch : Hq * Sq * D;
+    a.o_sh = out_strides ? out_strides->head : Sq * D;
+    a.o_st = out_strides ? out_strides->token : D;
+    a.batch = (int32_t)p->batch;
+    a.q_heads = (int32_t)Hq;
+    a.kv_heads = (int32_t)Hkv;
+    a.q_len = (int32_t)Sq;
+    a.kv_len = (int32_t)Skv;
+    a.query_start = (int32_t)p->query_start;
+    a.window = (int32_t)p->window;
+    a.score_shift = (int32_t)score_shift;
+    a.out_shift = (int32_t)out_shift;
+    a.q_tiles = (int32_t)ceil_div(Sq, kIntRows);
+    const int64_t items = a.q_tiles * Hq * p->batch;
+    if (items >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
+    const dim3 grid((unsigned)items);
+    if (D == 128)
+        hipLaunchKernelGGL(int_head_kernel<128>, grid, dim3(kIntThreads), 0, stream, a);
+    else if (D == 64)
+        hipLaunchKernelGGL(int_head_kernel<64>, grid, dim3(kIntThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(int_head_kernel<32>, grid, dim3(kIntThreads), 0, stream, a);
+    return launch_status();
+}
