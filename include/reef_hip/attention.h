@@ -48,7 +48,9 @@ typedef enum reef_status {
     /* a HIP runtime call failed. */
     REEF_HIP_ERROR = 4,
     /* well-formed but outside what the kernels implement (e.g. head_dim). */
-    REEF_UNSUPPORTED = 5
+    REEF_UNSUPPORTED = 5,
+    /* engine: std::overflow_error from safe_multiply / safe_add (util.hpp:81-131). */
+    REEF_OVERFLOW = 6
 } reef_status;
 
 /* Bits set in a status word by the kernels. */
@@ -56,6 +58,7 @@ typedef enum reef_status {
 #define REEF_STATUS_BIT_BAD_PAGE 0x2u
 #define REEF_STATUS_BIT_BAD_LENGTH 0x4u
 #define REEF_STATUS_BIT_CAPACITY 0x8u
+#define REEF_STATUS_BIT_OVERFLOW 0x10u
 
 typedef enum reef_scale_granularity {
     REEF_SCALE_PER_TENSOR = 0, /* one scale: scales[0] */
@@ -102,9 +105,36 @@ reef_status reef_dequantize_int8(const int8_t *q, int64_t n, int64_t group, cons
 
 /* Waits for the stream, reads a status word written by the kernels and maps
  * it: 0 -> REEF_OK, NON_FINITE -> REEF_NON_FINITE_INPUT, CAPACITY ->
- * REEF_CAPACITY, page/length bits -> REEF_INVALID_ARGUMENT (first match in
- * that order). Clears the word afterwards when clear != 0. */
+ * REEF_CAPACITY, OVERFLOW -> REEF_OVERFLOW, page/length bits ->
+ * REEF_INVALID_ARGUMENT (first match in that order). Clears the word afterwards
+ * when clear != 0. */
 reef_status reef_read_status_word(uint32_t *status_word, int clear, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * W8A8 projection: linear() with a QuantizedWeight (operator/linear.hpp:106-132).
+ * x [rows, in] fp32 (row r at x + r * x_row_stride) is quantized per row as
+ * quantize_rows does (quant.hpp:112-133), multiplied by the int8 weight
+ * [out, in] (row-major, the engine's layout) in exact int32, and
+ * y[r, c] = float(sum) * (row_scale[r] * w_scales[c]) (+ bias[c]), the engine's
+ * float steps in its order, each rounded on its own: bit-identical outputs. y is
+ * fp32 [rows, out] with row stride y_row_stride. in must be a multiple of 16.
+ * Non-finite input sets NON_FINITE; an infinite or NaN output sets OVERFLOW
+ * (the engine's std::overflow_error). The workspace holds the quantized rows.
+ */
+size_t reef_linear_w8a8_workspace_bytes(int64_t rows, int64_t in_features);
+
+reef_status reef_linear_w8a8(const float *x, int64_t rows, int64_t in_features,
+                             int64_t x_row_stride, const int8_t *weight, const float *w_scales,
+                             const float *bias, int64_t out_features, float *y,
+                             int64_t y_row_stride, void *workspace, size_t workspace_bytes,
+                             uint32_t *status_word, hipStream_t stream);
+
+/* The product and epilogue alone, on rows already quantized (xq [rows, in] packed,
+ * x_scales [rows]). */
+reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows,
+                           int64_t in_features, const int8_t *weight, const float *w_scales,
+                           const float *bias, int64_t out_features, float *y,
+                           int64_t y_row_stride, uint32_t *status_word, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Attention over int8 Q/K/V with an fp32 softmax and fp32 output.

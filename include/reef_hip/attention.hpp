@@ -48,6 +48,9 @@ inline void check(reef_status status, const char *what) {
         throw std::length_error("KV cache capacity exceeded");
     case REEF_UNSUPPORTED:
         throw unsupported(std::string(what) + ": not supported by the device kernels");
+    case REEF_OVERFLOW:
+        // util.hpp:117-123
+        throw std::overflow_error("safe_multiply product overflow");
     case REEF_HIP_ERROR:
     default:
         throw hip_error(std::string(what) + ": HIP runtime error");
@@ -135,6 +138,42 @@ inline void decode_paged(const reef_decode_params &p, const int8_t *q, const flo
                                            num_pages, context_lens, out, workspace,
                                            workspace_bytes, status_word, stream),
           "attention decode");
+}
+
+// Attention::append_kv_cache (attention.hpp:290-352) on the int8 cache, in place;
+// a full cache throws std::length_error like the engine once the status word is
+// checked.
+inline void append_kv_cache(const reef_kv_append_params &p, const float *k_new,
+                            const reef_strides *k_strides, const float *v_new,
+                            const reef_strides *v_strides, const int32_t *start_positions,
+                            int8_t *k_cache, int8_t *v_cache, float *k_scales, float *v_scales,
+                            int32_t *context_lens, uint32_t *status_word, hipStream_t stream) {
+    check(reef_kv_append_int8(&p, k_new, k_strides, v_new, v_strides, start_positions, k_cache,
+                              v_cache, k_scales, v_scales, context_lens, status_word, stream),
+          "append_kv_cache");
+}
+
+// attend_head_int8 (int8.hpp:250-279) for every (batch, head), bit-identical.
+inline void attend_int8_integer(const reef_attention_params &p, const int8_t *q,
+                                const reef_strides *q_strides, const int8_t *k,
+                                const reef_strides *k_strides, const int8_t *v,
+                                const reef_strides *v_strides, unsigned score_shift,
+                                const uint16_t *table, unsigned out_shift, int8_t *out,
+                                const reef_strides *out_strides, hipStream_t stream) {
+    check(reef_attention_int8_integer(&p, q, q_strides, k, k_strides, v, v_strides, score_shift,
+                                      table, out_shift, out, out_strides, stream),
+          "attend_head_int8");
+}
+
+// linear() with a QuantizedWeight (operator/linear.hpp:106-132), bit-identical.
+inline void linear_w8a8(const float *x, int64_t rows, int64_t in_features, int64_t x_row_stride,
+                        const int8_t *weight, const float *w_scales, const float *bias,
+                        int64_t out_features, float *y, int64_t y_row_stride, void *workspace,
+                        size_t workspace_bytes, uint32_t *status_word, hipStream_t stream) {
+    check(reef_linear_w8a8(x, rows, in_features, x_row_stride, weight, w_scales, bias,
+                           out_features, y, y_row_stride, workspace, workspace_bytes, status_word,
+                           stream),
+          "linear");
 }
 
 }  // namespace reef_hip

@@ -21,7 +21,7 @@ import os
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libreef_hip.so")
 
-OK, INVALID_ARGUMENT, NON_FINITE_INPUT, CAPACITY, HIP_ERROR, UNSUPPORTED = range(6)
+OK, INVALID_ARGUMENT, NON_FINITE_INPUT, CAPACITY, HIP_ERROR, UNSUPPORTED, OVERFLOW = range(7)
 PER_TENSOR, PER_HEAD, PER_TOKEN = 0, 1, 2
 ATTN_PRECISE_PV = 0x1
 PAGE = 16
@@ -32,7 +32,8 @@ EXPORTS = [
     "reef_attention_prefill_int8", "reef_qk_scores_i32",
     "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
     "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages", "reef_kv_append_int8",
-    "reef_kv_append_int8_paged", "reef_attention_int8_integer",
+    "reef_kv_append_int8_paged", "reef_attention_int8_integer", "reef_linear_w8a8_workspace_bytes",
+    "reef_linear_w8a8", "reef_gemm_w8a8",
 ]
 
 
@@ -60,8 +61,13 @@ class Unsupported(ReefError, NotImplementedError):
     pass
 
 
+class Overflow(ReefError, OverflowError):
+    pass
+
+
 _ERRORS = {INVALID_ARGUMENT: InvalidArgument, NON_FINITE_INPUT: NonFiniteInput,
-           CAPACITY: CapacityError, HIP_ERROR: HipError, UNSUPPORTED: Unsupported}
+           CAPACITY: CapacityError, HIP_ERROR: HipError, UNSUPPORTED: Unsupported,
+           OVERFLOW: Overflow}
 
 
 class Strides(C.Structure):
@@ -107,6 +113,10 @@ _SIGS = {
     "reef_attention_decode_int8_paged": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P,
                                          _I64, _I64, _P, _P, _P, C.c_size_t, _P, _P],
     "reef_kv_pack_v_pages": [_P, _I64, _I64, _P, _P],
+    "reef_linear_w8a8_workspace_bytes": [_I64, _I64],
+    "reef_linear_w8a8": [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, C.c_size_t, _P,
+                         _P],
+    "reef_gemm_w8a8": [_P, _P, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P],
     "reef_attention_int8_integer": [C.POINTER(AttentionParams), _P, C.POINTER(Strides), _P,
                                     C.POINTER(Strides), _P, C.POINTER(Strides), C.c_uint32, _P,
                                     C.c_uint32, _P, C.POINTER(Strides), _P],
@@ -469,3 +479,30 @@ def attention_int8_integer(q, k, v, table, *, score_shift, out_shift=8, query_st
         score_shift, _ptr(table.contiguous()), out_shift, _ptr(out), C.byref(so), _stream()),
         "attention_int8_integer")
     return out
+
+
+# --- W8A8 projection (operator/linear.hpp:106-132) ---------------------------------------
+
+def linear_w8a8(x, weight, w_scales, bias=None, status: StatusWord | None = None):
+    """y = linear(x, QuantizedWeight{weight, w_scales}, bias): x [rows, in] fp32,
+    weight [out, in] int8, w_scales [out] fp32, bias [out] fp32 or None. Rows are
+    quantized per row on the device; outputs are bit-identical to the engine's."""
+    torch = _torch()
+    _require(x, torch.float32, "x")
+    _require(weight, torch.int8, "weight")
+    _require(w_scales, torch.float32, "w_scales")
+    if x.dim() != 2 or x.stride(1) != 1 or weight.dim() != 2 or weight.shape[1] != x.shape[1]:
+        raise InvalidArgument("linear_w8a8 shapes: x [rows, in], weight [out, in]")
+    rows, fin = x.shape
+    fout = weight.shape[0]
+    n = lib().reef_linear_w8a8_workspace_bytes(rows, fin)
+    ws = torch.empty(n // 4 + 4, dtype=torch.float32, device=x.device)
+    y = torch.empty((rows, fout), dtype=torch.float32, device=x.device)
+    own = status or StatusWord(x.device)
+    check(lib().reef_linear_w8a8(
+        _ptr(x), rows, fin, x.stride(0), _ptr(weight.contiguous()), _ptr(w_scales.contiguous()),
+        _ptr(bias.contiguous()) if bias is not None else None, fout, _ptr(y), fout, _ptr(ws),
+        ws.numel() * 4, own.ptr, _stream()), "linear_w8a8")
+    if status is None:
+        own.check("linear_w8a8")
+    return y

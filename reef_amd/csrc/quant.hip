@@ -442,6 +442,7 @@ extern "C" reef_status reef_read_status_word(uint32_t *status_word, int clear,
     }
     if (word & REEF_STATUS_BIT_NON_FINITE) return REEF_NON_FINITE_INPUT;
     if (word & REEF_STATUS_BIT_CAPACITY) return REEF_CAPACITY;
+    if (word & REEF_STATUS_BIT_OVERFLOW) return REEF_OVERFLOW;
     if (word & (REEF_STATUS_BIT_BAD_PAGE | REEF_STATUS_BIT_BAD_LENGTH))
         return REEF_INVALID_ARGUMENT;
     return REEF_OK;
