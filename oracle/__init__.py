@@ -48,6 +48,8 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
     if os.path.isdir(os.environ.get("REEF_REFERENCE", "/root/reference/inference-engine")):
         subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+        if os.path.exists(os.path.join(HERE, "..", "reef_amd", "libreef_hip.so")):
+            subprocess.run(["make", "-s", "-C", HERE, "dropin"], check=True)
 
 
 def _load() -> C.CDLL:
