@@ -49,6 +49,8 @@ def parse():
                     help="prefill workload to time (c2, the headline, by default)")
     ap.add_argument("--decode", default="c3,c5b",
                     help="decode workloads to time (comma list of c3, c5b)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the W8A8 projection, integer-only head and KV-append lines")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run COPY_LAUNCHES copies of COPY_BYTES, then 3 launches of each "
                          "kernel, and exit (for rocprofv3 --pmc runs)")
@@ -197,6 +199,97 @@ def decode_c5b(torch, reef, W, steps, warmup, pools=3, num_splits=0):
     return cfg, cfg.kv_bytes(lens), wall_ms, kern_ms
 
 
+def bench_extras(torch, reef, W, steps):
+    """The paths beside attention, each on a workload of the benchmark's shapes:
+    the W8A8 projection of one tensor-parallel rank of a Llama-70B layer (4096
+    tokens, 8192 -> (8 + 2 * 1) * 128 features), the integer-only head on the
+    1x32x2048x128 causal prefill, and the KV-cache append of a 512-token prompt
+    chunk for 64 sequences x 8 KV heads."""
+    import ctypes as C
+    lib = reef.lib()
+    st = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    out = {}
+    # W8A8 projection
+    M, K, N = 4096, 8192, 1280
+    x = torch.randn((M, K), generator=g, device="cuda")
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    ws = torch.rand(N, device="cuda", generator=g) * 0.01
+    y = torch.empty((M, N), device="cuda")
+    wsp = torch.empty(lib.reef_linear_w8a8_workspace_bytes(M, K) // 4 + 4, device="cuda")
+
+    def lin():
+        rc = lib.reef_linear_w8a8(P(x), M, K, K, P(w), P(ws), None, N, P(y), N, P(wsp),
+                                  wsp.numel() * 4, None, st())
+        if rc != 0:
+            raise RuntimeError(f"linear status {rc}")
+    _, lin_ms = timed(torch, lin, steps, 3)
+    xq = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+    xs = torch.rand(M, device="cuda", generator=g) * 0.01
+
+    def gemm():
+        rc = lib.reef_gemm_w8a8(P(xq), P(xs), M, K, P(w), P(ws), None, N, P(y), N, None, st())
+        if rc != 0:
+            raise RuntimeError(f"gemm status {rc}")
+    _, gemm_ms = timed(torch, gemm, steps, 3)
+    ops = 2 * M * N * K
+    out["linear_w8a8"] = {"workload": f"{M} tokens x {K} -> {N} features",
+                          "ms": round(lin_ms, 5), "TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1),
+                          "gemm_only_ms": round(gemm_ms, 5),
+                          "gemm_only_TOPS": round(ops / (gemm_ms * 1e-3) / 1e12, 1),
+                          "frac_int8_peak": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+    del x, w, y, wsp, xq
+    # integer-only head, 1x32x2048x128 causal
+    cfg = W.CONFIGS["c2"]
+    qi = torch.randint(-127, 128, (1, 32, 2048, 128), dtype=torch.int8, device="cuda", generator=g)
+    ki = torch.randint(-127, 128, (1, 32, 2048, 128), dtype=torch.int8, device="cuda", generator=g)
+    vi = torch.randint(-127, 128, (1, 32, 2048, 128), dtype=torch.int8, device="cuda", generator=g)
+    # a table of the exp_table() form, round(32768 * e^(-d / 16)); the timing does
+    # not depend on its exact entries
+    table = torch.from_numpy(
+        np.rint(32768.0 * np.exp(-np.arange(256) / 16.0)).astype(np.uint16).view(np.int16)).cuda()
+    p = reef.AttentionParams(1, 32, 32, 2048, 2048, 128, 0, 0, 1.0, 1, 1, 0)
+    yi = torch.empty_like(qi)
+
+    def ihead():
+        rc = lib.reef_attention_int8_integer(C.byref(p), P(qi), None, P(ki), None, P(vi), None, 10,
+                                             P(table), 8, P(yi), None, st())
+        if rc != 0:
+            raise RuntimeError(f"integer head status {rc}")
+    _, ih_ms = timed(torch, ihead, max(5, steps // 4), 2)
+    iops = cfg.algorithmic_ops()
+    out["integer_head"] = {"workload": cfg.name + ", integer-only (int8.hpp)",
+                           "ms": round(ih_ms, 5), "TOPS": round(iops / (ih_ms * 1e-3) / 1e12, 1),
+                           "note": "three passes over the keys (max, sum, output)"}
+    del qi, ki, vi, yi
+    # KV append: a 512-token chunk for 64 sequences x 8 KV heads into an 8192-token cache
+    B, H, T, D, L = 64, 8, 512, 128, 8192
+    kf = torch.randn((B, H, T, D), device="cuda", generator=g)
+    vf = torch.randn((B, H, T, D), device="cuda", generator=g)
+    kc = torch.empty((B, H, L, D), dtype=torch.int8, device="cuda")
+    vc = torch.empty((B, H, L // 16, D, 16), dtype=torch.int8, device="cuda")
+    kcs = torch.empty((B, H, L), device="cuda")
+    vcs = torch.empty((B, H, L), device="cuda")
+    starts = torch.full((B,), 1024, dtype=torch.int32, device="cuda")
+    ap = reef.KvAppendParams(B, H, D, T, L)
+    sk = reef.Strides(*kf.stride()[:3])
+    sv = reef.Strides(*vf.stride()[:3])
+
+    def append():
+        rc = lib.reef_kv_append_int8(C.byref(ap), P(kf), C.byref(sk), P(vf), C.byref(sv), P(starts),
+                                     P(kc), P(vc), P(kcs), P(vcs), None, None, st())
+        if rc != 0:
+            raise RuntimeError(f"append status {rc}")
+    _, ap_ms = timed(torch, append, steps, 3)
+    ab = 2 * B * H * T * (4 * D + D + 4)
+    out["kv_append"] = {"workload": f"{T}-token chunk, {B} sequences x {H} KV heads, d {D}",
+                        "ms": round(ap_ms, 5), "GB/s": round(ab / (ap_ms * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(ab / (ap_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    return out
+
+
 COPY_BYTES = 1 << 30  # the calibration copy reads and writes this many bytes
 COPY_LAUNCHES = 3
 
@@ -325,6 +418,9 @@ def main():
                         "GB/s_wall": round(nbytes / (dwall * 1e-3) / 1e9, 1)})
             torch.cuda.empty_cache()
         rec["decode"] = dec
+    if not args.no_extra:
+        rec["extra"] = bench_extras(torch, reef, W, max(10, args.steps // 2))
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline(cfg, inputs, args.cpu_seconds)
     else:
