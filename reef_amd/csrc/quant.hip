@@ -242,6 +242,53 @@ __global__ __launch_bounds__(kQuantThreads) void token_quantize_regs(
     }
 }
 
+// Wide rows (256 < width / 4 <= 256 * PER): one block per row, PER float4 per
+// thread held in registers, the largest magnitude reduced across the block.
+template <int PER>
+__global__ __launch_bounds__(kQuantThreads) void token_quantize_wide(
+    const float *__restrict__ x, int32_t w4, int64_t row_stride, int8_t *__restrict__ q,
+    float *__restrict__ scales, uint32_t *status) {
+    __shared__ uint32_t partial[kQuantThreads / kWave];
+    const int64_t row = blockIdx.x;
+    const float4 *r = reinterpret_cast<const float4 *>(x + row * row_stride);
+    float4 v[PER];
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int col = threadIdx.x + j * kQuantThreads;
+        v[j] = col < w4 ? r[col] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t a = mag_bits(v[j].x), b = mag_bits(v[j].y), c = mag_bits(v[j].z),
+                 d = mag_bits(v[j].w);
+        a = a > b ? a : b;
+        c = c > d ? c : d;
+        a = a > c ? a : c;
+        m = m > a ? m : a;
+    }
+    m = wave_max_u32(m);
+    if (threadIdx.x % kWave == 0) partial[threadIdx.x / kWave] = m;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kQuantThreads / kWave; ++w) m = m > partial[w] ? m : partial[w];
+    const float scale = int8_scale(__uint_as_float(m));
+    char4 *out = reinterpret_cast<char4 *>(q + row * (int64_t)w4 * 4);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int col = threadIdx.x + j * kQuantThreads;
+        if (col < w4) {
+            char4 c;
+            c.x = quantize_int8(v[j].x, scale);
+            c.y = quantize_int8(v[j].y, scale);
+            c.z = quantize_int8(v[j].z, scale);
+            c.w = quantize_int8(v[j].w, scale);
+            out[col] = c;
+        }
+    }
+    if (threadIdx.x == 0) {
+        scales[row] = scale;
+        if (m >= 0x7f800000u) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
+    }
+}
+
 // General form: one wave per row, the row read twice.
 __global__ __launch_bounds__(kQuantThreads) void token_quantize(const float *__restrict__ x,
                                                                 int64_t rows, int64_t width,
@@ -401,6 +448,17 @@ extern "C" reef_status reef_quantize_int8_per_token(const float *x, int64_t rows
             else REEF_TOKEN_LAUNCH(64, 4);
         }
 #undef REEF_TOKEN_LAUNCH
+    } else if (vec && w4 <= 8 * kQuantThreads && rows < (int64_t(1) << 31)) {
+        const dim3 grid((unsigned)rows);
+        if (w4 <= 2 * kQuantThreads)
+            hipLaunchKernelGGL(token_quantize_wide<2>, grid, dim3(kQuantThreads), 0, stream, x,
+                               (int32_t)w4, row_stride, q, scales, status_word);
+        else if (w4 <= 4 * kQuantThreads)
+            hipLaunchKernelGGL(token_quantize_wide<4>, grid, dim3(kQuantThreads), 0, stream, x,
+                               (int32_t)w4, row_stride, q, scales, status_word);
+        else
+            hipLaunchKernelGGL(token_quantize_wide<8>, grid, dim3(kQuantThreads), 0, stream, x,
+                               (int32_t)w4, row_stride, q, scales, status_word);
     } else {
         const dim3 grid((unsigned)ceil_div(rows, kQuantThreads / kWave));
         hipLaunchKernelGGL(token_quantize, grid, dim3(kQuantThreads), 0, stream, x, rows, width,

@@ -105,7 +105,8 @@ def test_quantize_per_head_bit_exact_with_strides(reef):
     assert host(s)[5] == 1.0
 
 
-@pytest.mark.parametrize("rows,width", [(4096, 128), (7, 37), (300, 64), (3, 1)])
+@pytest.mark.parametrize("rows,width", [(4096, 128), (7, 37), (300, 64), (3, 1), (33, 96),
+                                        (40, 2048), (9, 5000), (17, 8192), (5, 8193)])
 def test_quantize_rows_bit_exact(reef, rows, width):
     case(f"quantize_rows {rows}x{width}")
     x = W.lcg_normal(23 + width, rows * width).reshape(rows, width)
