@@ -46,6 +46,7 @@ struct DecodeArgs {
     uint32_t *status;
     int32_t batch, q_heads, kv_heads, group;
     int32_t max_context, window, splits;
+    int32_t groups;  // partials per (sequence, head): one per workgroup of 4 splits
     int32_t max_blocks, num_pages;               // paged only
     int32_t q_gran;
     float score_scale;  // softmax_scale * log2(e)
@@ -127,7 +128,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
     const int col = lane & 15, grp = lane >> 4;
     const int split = blockIdx.x * kDecodeWaves + wave;
     const int kvh = blockIdx.y, b = blockIdx.z;
-    if (split >= a.splits) return;
+    // Every wave reaches the workgroup merge below, so none returns early; a wave
+    // past the last split, or whose split holds no keys, contributes nothing.
+    const bool in_range = split < a.splits;
 
     const int head = kvh * a.group + col;   // this lane's query head (live if col < group)
     const bool head_ok = col < a.group;
@@ -143,10 +146,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
     // DRAM accesses of the waves running together close.
     const int k_step = a.splits * kBlockKeys;
     const int k_begin = (lo / kBlockKeys + split) * kBlockKeys;
-    const int k_end = len;
+    const int k_end = in_range ? len : 0;
     const int n_pages = (len + kPage - 1) / kPage;
-    // A split with no keys of this sequence writes nothing; the combine skips it.
-    if (k_begin >= k_end) return;
 
     // q^T operand: 16 bytes of head `head` per 64-wide reduction step.
     i32x4 qop[KS];
@@ -299,18 +300,54 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
     // Row sums: this lane holds head col's partial over its 16 keys per block.
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
+
+    // The workgroup's 4 splits merge in LDS (log-sum-exp) into one partial, so the
+    // combine reads a quarter as many. Waves 1..3 hand over (max, sum, accumulator
+    // in value units) in a lane-linear layout; wave 0 merges and writes.
+    __shared__ f32x4 sO[kDecodeWaves - 1][DB][kWave];
+    __shared__ float2 sML[kDecodeWaves - 1][kWave];
+    if (wave > 0) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) sO[wave - 1][d][lane] = acc[d] * s_run;
+        sML[wave - 1][lane] = float2{m_run, l_run};
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    float mw[kDecodeWaves], lw[kDecodeWaves];
+    mw[0] = m_run;
+    lw[0] = l_run;
+#pragma unroll
+    for (int w = 1; w < kDecodeWaves; ++w) {
+        const float2 x = sML[w - 1][lane];
+        mw[w] = x.x;
+        lw[w] = x.y;
+    }
+    float m = mw[0];
+#pragma unroll
+    for (int w = 1; w < kDecodeWaves; ++w) m = fmaxf(m, mw[w]);
+    float e[kDecodeWaves], l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+        e[w] = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - m);
+        l += lw[w] * e[w];
+    }
     // acc[d][i] is (channel 16 d + 4 grp + i, head col); write live heads.
     const int64_t base_bh = (int64_t)b * a.q_heads + kvh * a.group;
+    const int g = blockIdx.x;  // this workgroup's partial
     if (head_ok) {
-        float *po = a.part_o + ((base_bh + col) * a.splits + split) * D;
+        float *po = a.part_o + ((base_bh + col) * a.groups + g) * D;
 #pragma unroll
-        for (int d = 0; d < DB; ++d)
-            *reinterpret_cast<f32x4 *>(po + 16 * d + 4 * grp) = acc[d] * s_run;
+        for (int d = 0; d < DB; ++d) {
+            f32x4 o = acc[d] * (s_run * e[0]);
+#pragma unroll
+            for (int w = 1; w < kDecodeWaves; ++w) o += sO[w - 1][d][lane] * e[w];
+            *reinterpret_cast<f32x4 *>(po + 16 * d + 4 * grp) = o;
+        }
     }
     if (head_ok && grp == 0) {
-        float *ml = a.part_ml + ((base_bh + col) * a.splits + split) * 2;
-        ml[0] = m_run;
-        ml[1] = l_run;
+        float *ml = a.part_ml + ((base_bh + col) * a.groups + g) * 2;
+        ml[0] = m;
+        ml[1] = l;
     }
 }
 
@@ -323,13 +360,16 @@ __global__ __launch_bounds__(64) void decode_combine(const float *__restrict__ p
                                                      DecodeArgs a, float *__restrict__ out) {
     const int64_t bh = blockIdx.x;
     const int lane = threadIdx.x;
-    const int splits = a.splits;
+    const int splits = a.groups;
     const int b = (int)(bh / a.q_heads);
     int len = a.context_lens ? a.context_lens[b] : a.max_context;
     if (len < 1 || len > a.max_context) len = 0;
     const int lo = a.window > 0 ? max(0, len - a.window) : 0;
-    // split s is live when block lo / 64 + s starts before len
-    const int live = len > 0 ? min(splits, (len + kBlockKeys - 1) / kBlockKeys - lo / kBlockKeys) : 0;
+    // split s is live when block lo / 64 + s starts before len; workgroup g (splits
+    // 4 g .. 4 g + 3) when its first split is
+    const int live_splits =
+        len > 0 ? min(a.splits, (len + kBlockKeys - 1) / kBlockKeys - lo / kBlockKeys) : 0;
+    const int live = (live_splits + kDecodeWaves - 1) / kDecodeWaves;
     const float *ml = part_ml + bh * splits * 2;
     const float *po = part_o + bh * splits * D;
     float o[D / 64];
@@ -411,6 +451,7 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
                           hipStream_t stream) {
     const int splits = default_splits(p);
     a.splits = splits;
+    a.groups = (int32_t)ceil_div(splits, kDecodeWaves);
     a.batch = (int32_t)p->batch;
     a.q_heads = (int32_t)p->q_heads;
     a.kv_heads = (int32_t)p->kv_heads;
@@ -436,7 +477,7 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
 }
 
 void set_workspace(DecodeArgs &a, const reef_decode_params *p, void *workspace) {
-    const int64_t rows = p->batch * p->q_heads * (int64_t)default_splits(p);
+    const int64_t rows = p->batch * p->q_heads * ceil_div(default_splits(p), kDecodeWaves);
     a.part_o = static_cast<float *>(workspace);
     a.part_ml = a.part_o + rows * p->head_dim;
 }
@@ -449,7 +490,7 @@ using namespace reef;
 extern "C" size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p) {
     if (!p || p->batch <= 0 || p->q_heads <= 0 || p->head_dim <= 0 || p->max_context <= 0)
         return 0;
-    const int64_t rows = p->batch * p->q_heads * (int64_t)default_splits(p);
+    const int64_t rows = p->batch * p->q_heads * ceil_div(default_splits(p), kDecodeWaves);
     return (size_t)(rows * (p->head_dim + 2) * sizeof(float));
 }
 
