@@ -373,6 +373,8 @@ def main():
         fns = {"c3": decode_c3, "c5b": decode_c5b}
         for fn in (fns[n] for n in args.decode.split(",") if n):
             fn(torch, reef, W, 3, 1)
+        if not args.no_extra:
+            bench_extras(torch, reef, W, 3)
         print(json.dumps({"profile_pass": True, "copy_bytes": COPY_BYTES,
                           "copy_launches": COPY_LAUNCHES}), flush=True)
         return
