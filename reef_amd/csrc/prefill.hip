@@ -421,23 +421,46 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int
             }
             };
 
-    if (n_tiles > 0) store_tile(0);
-    __syncthreads();
-    for (int it = 0; it < n_iter; ++it) {
+    // One pipeline step: the next tile's loads in flight during this tile's math,
+    // then its LDS stores. With `every_row` the tile is inside the visible range of
+    // every row of the workgroup, so no wave skips it or masks it: such steps run in
+    // a loop of their own with a single code path, which keeps the output
+    // accumulators in place (merging the masked and unmasked versions of a tile
+    // would copy all of them on every step).
+    auto step = [&](const int it, auto every_row_tag) {
+        constexpr bool every_row = decltype(every_row_tag)::value;
         const int kt = kt0 + it * kBN;
         const int buf = it & 1;
-        const bool mine = it < n_tiles;  // uniform over the group
-        if (it + 1 < n_tiles) load_tile(kt + kBN);  // in flight during this tile's math
-        if (mine && wave_active && kt <= wk_hi && kt + kBN - 1 >= wk_lo) {  // wave-uniform
-            // Tiles inside every row's visible range take the path without masks.
-            if (kt + kBN - 1 <= full_hi && kt >= full_lo)
-                tile_math(kt, buf, std::false_type{});
-            else
-                tile_math(kt, buf, std::true_type{});
+        if (it + 1 < n_tiles) load_tile(kt + kBN);
+        if constexpr (every_row) {
+            tile_math(kt, buf, std::false_type{});
+        } else {
+            const bool mine = it < n_tiles;  // uniform over the group
+            if (mine && wave_active && kt <= wk_hi && kt + kBN - 1 >= wk_lo) {  // wave-uniform
+                // Tiles inside every row's visible range take the path without masks.
+                if (kt + kBN - 1 <= full_hi && kt >= full_lo)
+                    tile_math(kt, buf, std::false_type{});
+                else
+                    tile_math(kt, buf, std::true_type{});
+            }
         }
         if (it + 1 < n_tiles) store_tile(buf ^ 1);
         __syncthreads();
-    }
+    };
+    // Steps [it_a, it_b): tiles every row of the workgroup sees whole. Rows past
+    // q_len (a partial last query tile) compute on zero queries and store nothing.
+    const int wg_full_lo = a.window > 0 ? a.query_start + r_last + 1 - a.window : 0;
+    const int wg_full_hi = min(a.query_start + q0, a.kv_len - 1);
+    const int it_a = max(0, wg_full_lo - kt0 + kBN - 1) / kBN;
+    const int span = wg_full_hi + 1 - kt0;  // keys from kt0 through wg_full_hi
+    const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kBN : 0));
+
+    if (n_tiles > 0) store_tile(0);
+    __syncthreads();
+    int it = 0;
+    for (; it < it_a; ++it) step(it, std::false_type{});
+    for (; it < it_b; ++it) step(it, std::true_type{});
+    for (; it < n_iter; ++it) step(it, std::false_type{});
 
     float l_tot = xor32_sum(l_run);
     if (SPLIT) {
