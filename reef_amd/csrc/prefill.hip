@@ -88,15 +88,28 @@ __device__ __forceinline__ float scale_of(const float *s, int gran, int b, int h
     return s[((int64_t)b * heads + h) * tokens + t];
 }
 
-// Two fp16 of keys (key0, key1) at one channel from the int8 bytes b0 (of key0)
-// and b1 (of key1) at byte `sel` of words w0 and w1 (already XORed with 0x80):
-// the byte gather leaves [b0, 0, b1, 0]; the 0x64 exponent bytes make each half
-// the fp16 1024 + (b + 128), and subtracting 1152 gives b exactly.
-__device__ __forceinline__ f16x2 int8_pair_to_f16(uint32_t w0, uint32_t w1, int sel) {
-    const uint32_t pick = (uint32_t)sel | (0x0cu << 8) | ((uint32_t)(4 + sel) << 16) | (0x0cu << 24);
-    const uint32_t bits = __builtin_amdgcn_perm(w1, w0, pick) | 0x64006400u;
-    return __builtin_bit_cast(f16x2, bits) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+// Two fp16 of keys (key0, key1) at one channel, packed [key0, key1], from the
+// int8 byte `sel` of words w0 (key0) and w1 (key1): each half is one
+// v_cvt_f16_i16 reading the sign-extended byte through a sub-dword operand
+// select (exact: every int8 is an fp16 integer), the second write keeping the
+// first half.
+#define REEF_CVT_PAIR(SEL)                                                                     \
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #SEL \
+        "\n\tv_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE "        \
+        "src0_sel:BYTE_" #SEL                                                                  \
+        : "=&v"(r)                                                                             \
+        : "v"(w0), "v"(w1))
+__device__ __forceinline__ uint32_t int8_pair_to_f16(uint32_t w0, uint32_t w1, int sel) {
+    uint32_t r;
+    switch (sel) {  // a constant once the caller's loop is unrolled
+    case 0: REEF_CVT_PAIR(0); break;
+    case 1: REEF_CVT_PAIR(1); break;
+    case 2: REEF_CVT_PAIR(2); break;
+    default: REEF_CVT_PAIR(3); break;
+    }
+    return r;
 }
+#undef REEF_CVT_PAIR
 
 // Work items are (query tile, batch x head), ranked heaviest first: the causal
 // rows of the last tile see the most keys.
@@ -241,18 +254,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int
 #pragma unroll
         for (int j = 0; j < KLOADS; ++j) *reinterpret_cast<i32x4 *>(sK + kdst[j]) = kreg[j];
         if (tid < VBLOCKS) {
-            uint32_t w[4][2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                w[i][0] = vreg[i].x ^ 0x80808080u;
-                w[i][1] = vreg[i].y ^ 0x80808080u;
-            }
+            const uint32_t w[4][2] = {{vreg[0].x, vreg[0].y}, {vreg[1].x, vreg[1].y},
+                                      {vreg[2].x, vreg[2].y}, {vreg[3].x, vreg[3].y}};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const f16x2 k01 = int8_pair_to_f16(w[0][j >> 2], w[1][j >> 2], j & 3);
-                const f16x2 k23 = int8_pair_to_f16(w[2][j >> 2], w[3][j >> 2], j & 3);
-                *reinterpret_cast<f16x4 *>(sVT + (8 * vdg + j) * VSTRIDE + 4 * vkg * 2) =
-                    f16x4{k01[0], k01[1], k23[0], k23[1]};
+                const uint32_t k01 = int8_pair_to_f16(w[0][j >> 2], w[1][j >> 2], j & 3);
+                const uint32_t k23 = int8_pair_to_f16(w[2][j >> 2], w[3][j >> 2], j & 3);
+                *reinterpret_cast<uint2 *>(sVT + (8 * vdg + j) * VSTRIDE + 4 * vkg * 2) =
+                    uint2{k01, k23};
             }
         }
         if (KV_TOKEN && wave == 0) {

@@ -224,6 +224,31 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
         assert err <= TOL, (precise, split, err)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_full_int8_range(reef, D):
+    """Raw int8 operands over the whole range, -128 included (a caller's own
+    codes, not the quantizer's): every V byte value must convert exactly."""
+    case(f"prefill full int8 range D{D}")
+    rng = np.random.default_rng(D)
+    B, H, S = 1, 2, 192
+    q = rand_i8(rng, (B, H, S, D), low=-128)
+    k = rand_i8(rng, (B, H, S, D), low=-128)
+    v = np.arange(B * H * S * D, dtype=np.int64).reshape(B, H, S, D)
+    v = ((v * 37) % 256 - 128).astype(np.int8)  # every byte value in every tile
+    qs = np.array([0.004], np.float32)
+    ks = np.array([0.003], np.float32)
+    vs = np.array([0.01], np.float32)
+    p = oracle.Problem(B, H, H, S, S, D, softmax_scale=1 / math.sqrt(D),
+                       q_granularity=0, kv_granularity=0)
+    gold = oracle.attention_int8(p, q, k, v, qs, ks, vs)
+    for precise in (False, True):
+        out = host(reef.attention_prefill(gpu(q), gpu(k), gpu(v), gpu(qs), gpu(ks), gpu(vs),
+                                          q_granularity=0, kv_granularity=0, precise=precise))
+        err = np.abs(out - gold).max()
+        print(f"precise={precise} max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL
+
+
 def test_prefill_rejects_bad_arguments(reef):
     case("prefill argument errors")
     z = torch.zeros((1, 1, 8, 128), dtype=torch.int8, device="cuda")
