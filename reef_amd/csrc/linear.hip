@@ -7,8 +7,12 @@
 // so the outputs are bit-identical.
 //
 // Tiling: a workgroup of 4 waves owns a 128 x 128 output tile; each wave a
-// 64 x 64 quarter as 2 x 2 blocks of 32 x 32. The K loop steps 64 bytes at a time
-// through two LDS stages, loads for the next step in flight during this one.
+// 64 x 64 quarter as 2 x 2 blocks of 32 x 32. K advances 64 bytes per step through
+// kStages LDS stages filled by direct-to-LDS buffer loads issued kStages - 1 steps
+// ahead, so a step's matrix work never waits on memory latency (no staging
+// registers, no LDS store instructions). Workgroups are numbered so that each XCD
+// (which receives every eighth workgroup) takes a contiguous run of tiles, rows of
+// tiles sharing their input rows in that XCD's L2.
 #include <algorithm>
 #include <cmath>
 
@@ -18,9 +22,23 @@ namespace reef {
 namespace {
 
 constexpr int kGemmThreads = 256;
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kRowBytes = kBK + 16;  // LDS row stride: rows r and r + 8 share no banks
-constexpr int kTileBytes = kBM * kRowBytes;
+constexpr int kXcds = 8;
+#ifndef REEF_GEMM_BN
+#define REEF_GEMM_BN 128
+#endif
+#ifndef REEF_GEMM_BK
+#define REEF_GEMM_BK 128
+#endif
+#ifndef REEF_GEMM_STAGES
+#define REEF_GEMM_STAGES 2
+#endif
+constexpr int kBM = 128, kBN = REEF_GEMM_BN;  // output tile: rows x out features
+constexpr int kNB = kBN / 64;                 // 32-wide column blocks per wave
+constexpr int kBK = REEF_GEMM_BK;             // bytes of K per step
+constexpr int kStages = REEF_GEMM_STAGES;
+constexpr int kABytes = kBM * kBK, kBBytes = kBN * kBK;  // operand tiles of one stage
+constexpr int kChunks = kBK / 16;             // 16-byte chunks per tile row
+constexpr int kRowsPerBlock = 1024 / kBK;     // tile rows per 1 KB direct load
 
 struct GemmArgs {
     const int8_t *x;  // [rows, in] quantized rows, row stride in
@@ -31,96 +49,128 @@ struct GemmArgs {
     float *y;
     int64_t y_stride;
     int32_t rows, in, out;
-    int32_t n_tiles;  // output tiles along out
+    int32_t m_tiles, n_tiles;
     uint32_t *status;
 };
 
+// Chunk c (16 bytes) of tile row r sits at 16 * (c ^ s(r)) in the row, s(r) the row
+// bits above those that already separate rows within 256 bytes: the 16 lanes that
+// read one chunk column of 16 consecutive rows hit 16 distinct bank groups.
+__device__ __forceinline__ int chunk_pos(int r, int c) {
+    constexpr int rows256 = 256 / kBK;  // rows whose chunks c fall in distinct bank groups
+    return c ^ ((r / rows256) & (kChunks - 1));
+}
+
 __global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t smem[2][2][kTileBytes];  // [stage][A|B]
+    __shared__ __attribute__((aligned(16))) int8_t smem[kStages][kABytes + kBBytes];  // [stage] A, B
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int col = lane & 31, grp = lane >> 5;
-    const int tm = (int)blockIdx.x / a.n_tiles, tn = (int)blockIdx.x % a.n_tiles;
+
+    // Workgroup i runs on XCD i % 8; give XCD x the contiguous tiles
+    // [start(x), start(x) + count(x)), tiles along `out` fastest.
+    const int T = (int)gridDim.x, g = (int)blockIdx.x;
+    const int x = g % kXcds, per = T / kXcds, rem = T % kXcds;
+    const int t = x * per + min(x, rem) + g / kXcds;
+    const int tm = t / a.n_tiles, tn = t % a.n_tiles;
     const int m0 = tm * kBM, n0 = tn * kBN;
 
-    // Loads: each thread moves two 16-byte chunks of A and two of B per K step:
-    // chunk c = tid + 256 j is row c / 4, bytes (c % 4) * 16. Rows past the end and
-    // bytes past `in` read zeros (buffer resource bounds).
-    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)((int64_t)a.rows * a.in));
-    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w, (uint32_t)((int64_t)a.out * a.in));
-    uint32_t aoff[2], boff[2];
-    int dst[2];
-    bool a_ok[2], b_ok[2];
+    // Direct loads: wave w fills 1 KB blocks w, w + 4, ... of each operand tile;
+    // lane L of block b writes tile row kRowsPerBlock b + L / kChunks at position
+    // L % kChunks, which holds chunk chunk_pos(row, L % kChunks). Rows past the end
+    // and chunks past `in` read zeros: their offset is set beyond the buffer.
+    constexpr int PA = kABytes / 1024 / 4, PB = kBBytes / 1024 / 4;  // blocks per wave
+    const uint32_t xbytes = (uint32_t)((int64_t)a.rows * a.in);
+    const uint32_t wbytes = (uint32_t)((int64_t)a.out * a.in);
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, xbytes);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w, wbytes);
+    uint32_t aoff[PA], boff[PB];
+    // (every block row of a wave has the same chunk position, so one k offset each)
+    const int kch = 16 * chunk_pos(kRowsPerBlock * wave + lane / kChunks, lane % kChunks);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int c = tid + kGemmThreads * j, r = c >> 2, kb = (c & 3) * 16;
-        a_ok[j] = m0 + r < a.rows;
-        b_ok[j] = n0 + r < a.out;
-        aoff[j] = (uint32_t)((int64_t)(a_ok[j] ? m0 + r : 0) * a.in + kb);
-        boff[j] = (uint32_t)((int64_t)(b_ok[j] ? n0 + r : 0) * a.in + kb);
-        dst[j] = r * kRowBytes + kb;
+    for (int i = 0; i < PA; ++i) {
+        const int r = kRowsPerBlock * (wave + 4 * i) + lane / kChunks;
+        aoff[i] = m0 + r < a.rows ? (uint32_t)((int64_t)(m0 + r) * a.in + kch) : xbytes;
     }
-    i32x4 ra[2], rb[2];
-    auto load = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            // a k offset past `in` (the last partial step) reads zeros
-            const bool in_k = k0 + (int)((tid + kGemmThreads * j) & 3) * 16 < a.in;
-            ra[j] = (a_ok[j] && in_k) ? __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[j], k0, 0)
-                                      : i32x4{0, 0, 0, 0};
-            rb[j] = (b_ok[j] && in_k) ? __builtin_amdgcn_raw_buffer_load_b128(wr, boff[j], k0, 0)
-                                      : i32x4{0, 0, 0, 0};
-        }
-    };
-    auto store = [&](int stage) {
+    for (int i = 0; i < PB; ++i) {
+        const int r = kRowsPerBlock * (wave + 4 * i) + lane / kChunks;
+        boff[i] = n0 + r < a.out ? (uint32_t)((int64_t)(n0 + r) * a.in + kch) : wbytes;
+    }
+    const int steps = (a.in + kBK - 1) / kBK;
+    auto issue = [&](int s) {  // K step s (clamped to the last) into stage s % kStages
+        const int k0 = min(s, steps - 1) * kBK;
+        int8_t *sa = smem[s % kStages];
+        int8_t *sb = sa + kABytes;
+        const bool in_k = k0 + kch < a.in;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            *reinterpret_cast<i32x4 *>(&smem[stage][0][dst[j]]) = ra[j];
-            *reinterpret_cast<i32x4 *>(&smem[stage][1][dst[j]]) = rb[j];
-        }
+        for (int i = 0; i < PA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(sa + 1024 * (wave + 4 * i)), 16,
+                in_k ? aoff[i] : xbytes, k0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wr, (__attribute__((address_space(3))) void *)(sb + 1024 * (wave + 4 * i)), 16,
+                in_k ? boff[i] : wbytes, k0, 0, 0);
     };
 
-    i32x16 acc[2][2];
+    // Operand reads: row 64 wm + 32 i + col (A) or 32 (kNB wn + j) + col (B), chunk
+    // 2 ks + grp; the swizzle depends on bits 2-3 of the row, i.e. of col.
+    int rpos[kBK / 32];
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) rpos[ks] = 16 * chunk_pos(col, 2 * ks + grp);
+    const int arow = (64 * wm + col) * kBK, brow = (32 * kNB * wn + col) * kBK;
+
+    i32x16 acc[2][kNB];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = i32x16{};
+        for (int j = 0; j < kNB; ++j) acc[i][j] = i32x16{};
 
-    const int steps = (a.in + kBK - 1) / kBK;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        const int stage = s & 1;
-        if (s + 1 < steps) load((s + 1) * kBK);
-        const int8_t *sa = smem[stage][0];
-        const int8_t *sb = smem[stage][1];
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s) issue(s);
+    for (int k = 0; k < steps; ++k) {
+        // Each wave has issued PA + PB loads per step; those of the kStages - 2 later
+        // steps may still be in flight, this step's must have landed. (s_waitcnt
+        // fields: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8; 0xf70 leaves
+        // the other two unconstrained.)
+        constexpr int kInFlight = (PA + PB) * (kStages - 2);
+        static_assert(kInFlight < 64, "vmcnt fits");
+        __builtin_amdgcn_s_waitcnt(0xf70 | (kInFlight & 15) | ((kInFlight >> 4) << 14));
+        // All waves' loads of step k are in LDS and their reads of step k - 1 are
+        // done (consumed by the matrix instructions), so stage (k - 1) is free. A
+        // bare barrier: __syncthreads() would also wait for every load in flight.
+        __builtin_amdgcn_s_barrier();
+        issue(k + kStages - 1);
+        const int8_t *sa = smem[k % kStages];
+        const int8_t *sb = sa + kABytes;
 #pragma unroll
         for (int ks = 0; ks < kBK / 32; ++ks) {
-            i32x4 aop[2], bop[2];
+            i32x4 aop[2], bop[kNB];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                aop[i] = *reinterpret_cast<const i32x4 *>(
-                    sa + (64 * wm + 32 * i + col) * kRowBytes + 32 * ks + 16 * grp);
-                bop[i] = *reinterpret_cast<const i32x4 *>(
-                    sb + (64 * wn + 32 * i + col) * kRowBytes + 32 * ks + 16 * grp);
-            }
+            for (int i = 0; i < 2; ++i)
+                aop[i] = *reinterpret_cast<const i32x4 *>(sa + arow + 32 * i * kBK + rpos[ks]);
+#pragma unroll
+            for (int j = 0; j < kNB; ++j)
+                bop[j] = *reinterpret_cast<const i32x4 *>(sb + brow + 32 * j * kBK + rpos[ks]);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma_32x32x32_i8(aop[i], bop[j], acc[i][j]);
+                for (int j = 0; j < kNB; ++j) acc[i][j] = mfma_32x32x32_i8(aop[i], bop[j], acc[i][j]);
         }
-        if (s + 1 < steps) store(stage ^ 1);
-        __syncthreads();
     }
+    // The trailing loads of the clamped last steps must land before the workgroup's
+    // LDS can be handed to another workgroup.
+    __builtin_amdgcn_s_waitcnt(0xf70);
 
-    // Epilogue: lane holds output column n0 + 64 wn + 32 j + col and, in register
+    // Epilogue: lane holds output column n0 + 32 (kNB wn + j) + col and, in register
     // 4 q + e, row m0 + 64 wm + 32 i + 8 q + 4 grp + e.
     bool bad = false;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + 64 * wn + 32 * j + col;
+    for (int j = 0; j < kNB; ++j) {
+        const int n = n0 + 32 * (kNB * wn + j) + col;
         if (n >= a.out) continue;
         const float wsc = a.ws[n];
         const float bn = a.bias ? a.bias[n] : 0.0f;
@@ -159,8 +209,9 @@ reef_status launch_gemm(const int8_t *xq, const float *xs, int64_t rows, int64_t
     a.in = (int32_t)in;
     a.out = (int32_t)out;
     a.n_tiles = (int32_t)ceil_div(out, kBN);
+    a.m_tiles = (int32_t)ceil_div(rows, kBM);
     a.status = status;
-    const int64_t tiles = ceil_div(rows, kBM) * a.n_tiles;
+    const int64_t tiles = (int64_t)a.m_tiles * a.n_tiles;
     hipLaunchKernelGGL(gemm_w8a8_kernel, dim3((unsigned)tiles), dim3(kGemmThreads), 0, stream, a);
     return launch_status();
 }
