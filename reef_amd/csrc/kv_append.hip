@@ -3,11 +3,13 @@
 // The engine's Attention::append_kv_cache (attention.hpp:290-352) copies the
 // whole fp32 cache into a new buffer on every call, one (batch, head) block at a
 // time, so that the new positions land at the end of each block. Here the cache
-// is preallocated to its capacity and stays in place: one wave quantizes one new
-// key row and one new value row per token (quantize_rows, quant.hpp:112-133,
-// bit-identical codes and scales) and writes them at the sequence's next
-// positions, K token-major and V into the transposed 16-token pages the decode
-// kernel reads. The capacity check of attention.hpp:321-327 becomes a status
+// is preallocated to its capacity and stays in place. One workgroup fills one
+// 16-token cache page of one (sequence, KV head) with the new tokens that fall
+// in it: each wave quantizes key and value rows (quantize_rows,
+// quant.hpp:112-133, bit-identical codes and scales) into LDS, K token-major and
+// V already transposed, and the page then leaves in 16-byte stores, whole pages
+// as they are laid out in the cache (K [16, D], V [D, 16], the layout the decode
+// kernel reads). The capacity check of attention.hpp:321-327 becomes a status
 // bit, since the lengths live on the device.
 #include "reef_common.hpp"
 
@@ -15,7 +17,8 @@ namespace reef {
 namespace {
 
 constexpr int kPage = 16;
-constexpr int kAppendThreads = 256;  // one wave per (batch, kv head, new token)
+constexpr int kAppendThreads = 256;  // 4 waves per (batch, kv head, cache page)
+constexpr int kAppendWaves = kAppendThreads / kWave;
 
 struct AppendArgs {
     const float *k, *v;
@@ -55,45 +58,72 @@ __device__ __forceinline__ float quantize_row(const float *src, int lane, bool &
 
 template <int D, bool PAGED>
 __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t rows = (int64_t)a.batch * a.kv_heads * a.new_tokens;
-    const int64_t row = (int64_t)blockIdx.x * (kAppendThreads / kWave) + threadIdx.x / kWave;
-    if (row >= rows) return;
-    const int t = (int)(row % a.new_tokens);
-    const int64_t bh = row / a.new_tokens;
-    const int kvh = (int)(bh % a.kv_heads);
-    const int b = (int)(bh / a.kv_heads);
+    __shared__ __attribute__((aligned(16))) int8_t sK[kPage * D];   // [slot][channel]
+    __shared__ __attribute__((aligned(16))) int8_t sVT[D * kPage];  // [channel][slot]
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.z, kvh = blockIdx.y;
     const int start = a.start[b];
     // attention.hpp:321-327: the whole append of a sequence fits or none of it is written.
     if (start < 0 || start > a.max_context - a.new_tokens) {
-        if (t == 0 && kvh == 0 && lane == 0)
+        if (blockIdx.x == 0 && kvh == 0 && tid == 0)
             flag_status(a.status, start < 0 ? REEF_STATUS_BIT_BAD_LENGTH : REEF_STATUS_BIT_CAPACITY);
         return;
     }
-    const int pos = start + t;
-    const int slot = pos % kPage;
+    // This workgroup's page and the positions [p_lo, p_hi) of new tokens in it.
+    const int page_idx = start / kPage + (int)blockIdx.x;
+    const int p_lo = max(start, page_idx * kPage);
+    const int p_hi = min(start + a.new_tokens, (page_idx + 1) * kPage);
+    if (p_lo >= p_hi) return;  // past the appended range (uniform over the workgroup)
     int64_t page_base;  // index of this (page, kv head) in units of 16-token pages
     if (PAGED) {
-        const int page = a.table[(int64_t)b * a.max_blocks + pos / kPage];
+        const int page = a.table[(int64_t)b * a.max_blocks + page_idx];
         if (page < 0 || page >= a.num_pages) {
-            if (lane == 0) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
+            if (tid == 0) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
             return;
         }
         page_base = (int64_t)page * a.kv_heads + kvh;
     } else {
-        page_base = ((int64_t)b * a.kv_heads + kvh) * (a.max_context / kPage) + pos / kPage;
+        page_base = ((int64_t)b * a.kv_heads + kvh) * (a.max_context / kPage) + page_idx;
     }
-    int8_t *krow = a.k_dst + (page_base * kPage + slot) * D;
-    int8_t *vpage = a.v_dst + page_base * D * kPage + slot;
-    bool bad_k, bad_v;
-    const float ks = quantize_row<D>(a.k + b * a.k_sb + kvh * a.k_sh + (int64_t)t * a.k_st, lane,
-                                     bad_k, [&](int d, int8_t c) { krow[d] = c; });
-    const float vs = quantize_row<D>(a.v + b * a.v_sb + kvh * a.v_sh + (int64_t)t * a.v_st, lane,
-                                     bad_v, [&](int d, int8_t c) { vpage[d * kPage] = c; });
-    if (lane == 0) {
-        a.ks_dst[page_base * kPage + slot] = ks;
-        a.vs_dst[page_base * kPage + slot] = vs;
-        if (bad_k || bad_v) flag_status(a.status, REEF_STATUS_BIT_NON_FINITE);
+    // Wave w quantizes slots w, w + 4, w + 8, w + 12 of the page.
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < kPage / kAppendWaves; ++i) {
+        const int slot = wave + kAppendWaves * i;
+        const int pos = page_idx * kPage + slot;
+        if (pos < p_lo || pos >= p_hi) continue;  // wave-uniform
+        const int t = pos - start;
+        bool bad_k, bad_v;
+        const float ks = quantize_row<D>(a.k + b * a.k_sb + kvh * a.k_sh + (int64_t)t * a.k_st,
+                                         lane, bad_k, [&](int d, int8_t c) { sK[slot * D + d] = c; });
+        const float vs = quantize_row<D>(a.v + b * a.v_sb + kvh * a.v_sh + (int64_t)t * a.v_st,
+                                         lane, bad_v, [&](int d, int8_t c) { sVT[d * kPage + slot] = c; });
+        if (lane == 0) {
+            a.ks_dst[page_base * kPage + slot] = ks;
+            a.vs_dst[page_base * kPage + slot] = vs;
+        }
+        bad |= bad_k || bad_v;
+    }
+    if (bad && lane == 0) flag_status(a.status, REEF_STATUS_BIT_NON_FINITE);
+    __syncthreads();
+    int8_t *kpage = a.k_dst + page_base * kPage * D;
+    int8_t *vpage = a.v_dst + page_base * D * kPage;
+    if (p_hi - p_lo == kPage) {
+        // A whole page: 16-byte copies of both LDS images.
+        for (int o = 16 * tid; o < kPage * D; o += 16 * kAppendThreads) {
+            *reinterpret_cast<i32x4 *>(kpage + o) = *reinterpret_cast<const i32x4 *>(sK + o);
+            *reinterpret_cast<i32x4 *>(vpage + o) = *reinterpret_cast<const i32x4 *>(sVT + o);
+        }
+    } else {
+        // A partial page (the first or last of the append): only its new slots
+        // change; the others hold earlier tokens.
+        const int s_lo = p_lo - page_idx * kPage, s_hi = p_hi - page_idx * kPage;
+        for (int o = tid; o < kPage * D; o += kAppendThreads) {
+            const int ks = o / D, vs = o % kPage;
+            if (ks >= s_lo && ks < s_hi) kpage[o] = sK[o];
+            if (vs >= s_lo && vs < s_hi) vpage[o] = sVT[o];
+        }
     }
 }
 
@@ -119,8 +149,8 @@ reef_status prepare(const reef_kv_append_params *p, const float *k_new, const re
     // attention.hpp:321-327: an append longer than the whole cache can never fit.
     if (p->new_tokens > p->max_context) return REEF_CAPACITY;
     if (p->head_dim != 64 && p->head_dim != 128) return REEF_UNSUPPORTED;
-    if (p->max_context >= (int64_t(1) << 30) || p->batch >= (int64_t(1) << 24) ||
-        p->batch * p->kv_heads * p->new_tokens >= (int64_t(1) << 31) / kWave)
+    // (grid: pages x kv heads x batch)
+    if (p->max_context >= (int64_t(1) << 30) || p->batch > 65535 || p->kv_heads > 65535)
         return REEF_UNSUPPORTED;
     const int64_t D = p->head_dim, H = p->kv_heads, T = p->new_tokens;
     const auto strides = [&](const reef_strides *s, int64_t &sb, int64_t &sh, int64_t &st) {
@@ -152,8 +182,10 @@ template <bool PAGED>
 reef_status launch(const reef_kv_append_params *p, AppendArgs &a, int32_t *context_lens,
                    uint32_t *status_word, hipStream_t stream) {
     a.status = status_word;
-    const int64_t rows = p->batch * p->kv_heads * p->new_tokens;
-    const dim3 grid((unsigned)ceil_div(rows, kAppendThreads / kWave));
+    // pages an append of new_tokens can touch: ceil(new_tokens / 16) + 1 when it
+    // starts inside a page
+    const dim3 grid((unsigned)(ceil_div(p->new_tokens, kPage) + 1), (unsigned)p->kv_heads,
+                    (unsigned)p->batch);
     if (p->head_dim == 128)
         hipLaunchKernelGGL((kv_append<128, PAGED>), grid, dim3(kAppendThreads), 0, stream, a);
     else
