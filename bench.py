@@ -88,6 +88,9 @@ def prefill_launcher(torch, reef, cfg, q, k, v, qs, ks, vs, out):
             C.byref(sk), C.c_void_p(v.data_ptr()), C.byref(sv), C.c_void_p(qs.data_ptr()),
             C.c_void_p(ks.data_ptr()), C.c_void_p(vs.data_ptr()), C.c_void_p(out.data_ptr()),
             C.byref(so))
+    # The balanced schedule's workspace: zero-filled once, left zero-filled by every launch.
+    ws = reef.prefill_workspace(p, q.device)
+    args = args + (C.c_void_p(ws.data_ptr()), ws.numel())
     fn = lib.reef_attention_prefill_int8
 
     def launch():

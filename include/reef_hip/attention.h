@@ -160,13 +160,22 @@ typedef struct reef_attention_params {
  * causal_visibility (:82-100). q [B, Hq, q_len, D], k and v [B, Hkv, kv_len, D],
  * out fp32 [B, Hq, q_len, D], each with optional strides. Requires
  * query_start + q_len <= kv_len, so that every row sees a key (the engine
- * throws for a row with none, activation.hpp:204-207). */
+ * throws for a row with none, activation.hpp:204-207).
+ *
+ * workspace (optional, 256-byte aligned, at least
+ * reef_attention_prefill_workspace_bytes(p) bytes; NULL/0 allowed) lets grids
+ * with few query tiles per compute unit split the causal work evenly over the
+ * GPU: it must be zero-filled before its first use, and every call leaves it
+ * zero-filled. Calls that may run at the same time need separate workspaces. */
+size_t reef_attention_prefill_workspace_bytes(const reef_attention_params *p);
+
 reef_status reef_attention_prefill_int8(const reef_attention_params *p, const int8_t *q,
                                         const reef_strides *q_strides, const int8_t *k,
                                         const reef_strides *k_strides, const int8_t *v,
                                         const reef_strides *v_strides, const float *q_scales,
                                         const float *k_scales, const float *v_scales, float *out,
-                                        const reef_strides *out_strides, hipStream_t stream);
+                                        const reef_strides *out_strides, void *workspace,
+                                        size_t workspace_bytes, hipStream_t stream);
 
 /* Bit-exact hook: the int32 score accumulators q . k^T (tensor.hpp:210-246
  * with int8 inputs and int32 sums), computed by the same MFMA tile code as the

@@ -100,13 +100,20 @@ inline void quantize_per_head(const float *x, int64_t batch, int64_t heads, int6
 // launch: the engine's query_start is kv_len - q_len (attention.hpp:415) and
 // its window is LocalAttention's (attention.hpp:223-261), 0 for GlobalAttention.
 // softmax_scale 1 reproduces the engine's unscaled scores (attention.hpp:104).
+// The optional workspace (prefill_workspace_bytes(p) bytes, zero-filled once
+// before first use) balances launches with few query tiles per compute unit.
+inline size_t prefill_workspace_bytes(const reef_attention_params &p) {
+    return reef_attention_prefill_workspace_bytes(&p);
+}
+
 inline void context(const reef_attention_params &p, const int8_t *q, const reef_strides *q_strides,
                     const int8_t *k, const reef_strides *k_strides, const int8_t *v,
                     const reef_strides *v_strides, const float *q_scales, const float *k_scales,
                     const float *v_scales, float *out, const reef_strides *out_strides,
-                    hipStream_t stream) {
+                    hipStream_t stream, void *workspace = nullptr, size_t workspace_bytes = 0) {
     check(reef_attention_prefill_int8(&p, q, q_strides, k, k_strides, v, v_strides, q_scales,
-                                      k_scales, v_scales, out, out_strides, stream),
+                                      k_scales, v_scales, out, out_strides, workspace,
+                                      workspace_bytes, stream),
           "attention context");
 }
 

@@ -29,7 +29,7 @@ PAGE = 16
 EXPORTS = [
     "reef_quantize_int8_per_tensor", "reef_quantize_int8_per_head",
     "reef_quantize_int8_per_token", "reef_dequantize_int8", "reef_read_status_word",
-    "reef_attention_prefill_int8", "reef_qk_scores_i32",
+    "reef_attention_prefill_workspace_bytes", "reef_attention_prefill_int8", "reef_qk_scores_i32",
     "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
     "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages", "reef_kv_append_int8",
     "reef_kv_append_int8_paged", "reef_attention_int8_integer", "reef_linear_w8a8_workspace_bytes",
@@ -103,9 +103,10 @@ _SIGS = {
     "reef_quantize_int8_per_token": [_P, _I64, _I64, _I64, _P, _P, _P, _P],
     "reef_dequantize_int8": [_P, _I64, _I64, _P, _P, _P],
     "reef_read_status_word": [_P, C.c_int, _P],
+    "reef_attention_prefill_workspace_bytes": [C.POINTER(AttentionParams)],
     "reef_attention_prefill_int8": [C.POINTER(AttentionParams), _P, C.POINTER(Strides), _P,
                                     C.POINTER(Strides), _P, C.POINTER(Strides), _P, _P, _P, _P,
-                                    C.POINTER(Strides), _P],
+                                    C.POINTER(Strides), _P, C.c_size_t, _P],
     "reef_qk_scores_i32": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "reef_attention_decode_workspace_bytes": [C.POINTER(DecodeParams)],
     "reef_attention_decode_int8": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -266,14 +267,34 @@ def dequantize(q, scales, group: int):
 
 # --- attention ------------------------------------------------------------------------
 
+_PREFILL_WS = {}
+
+
+def prefill_workspace(params: AttentionParams, device):
+    """The zero-filled workspace of the balanced prefill schedule, one per (device,
+    stream): every launch leaves it zero-filled, so the next launch on that stream
+    reuses it."""
+    torch = _torch()
+    n = lib().reef_attention_prefill_workspace_bytes(C.byref(params))
+    key = (torch.device(device).index, _stream().value)
+    ws = _PREFILL_WS.get(key)
+    if ws is None or ws.numel() < n:
+        ws = torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
+        _PREFILL_WS[key] = ws
+    return ws
+
+
 def attention_prefill(q, k, v, q_scales, k_scales, v_scales, *, query_start=None, window=0,
                       softmax_scale=None, q_granularity=PER_HEAD, kv_granularity=PER_HEAD,
-                      precise=False, out=None):
+                      precise=False, out=None, workspace=None):
     """Attention::context (attention.hpp:374-432) over int8 heads in one launch.
 
     q [B, Hq, Sq, D], k and v [B, Hkv, Skv, D] int8 (contiguous head_dim, any other
     strides); scales by granularity. softmax_scale defaults to 1/sqrt(D); pass 1.0
-    for the engine's unscaled scores. Returns fp32 [B, Hq, Sq, D].
+    for the engine's unscaled scores. Returns fp32 [B, Hq, Sq, D]. workspace: None
+    takes this stream's cached one (prefill_workspace), False passes none (grids
+    with few query tiles then take the unbalanced kernels), or a zero-filled uint8
+    tensor of reef_attention_prefill_workspace_bytes bytes.
     """
     torch = _torch()
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
@@ -292,10 +313,14 @@ def attention_prefill(q, k, v, q_scales, k_scales, v_scales, *, query_start=None
     if out is None:
         out = torch.empty((B, Hq, Sq, D), dtype=torch.float32, device=q.device)
     qs, ks, vs, os_ = _strides4(q), _strides4(k), _strides4(v), _strides4(out)
+    if workspace is None:
+        workspace = prefill_workspace(p, q.device)
+    ws_ptr, ws_n = (None, 0) if workspace is False else (_ptr(workspace), workspace.numel()
+                                                          * workspace.element_size())
     check(lib().reef_attention_prefill_int8(
         C.byref(p), _ptr(q), C.byref(qs), _ptr(k), C.byref(ks), _ptr(v), C.byref(vs),
         _ptr(q_scales.contiguous()), _ptr(k_scales.contiguous()), _ptr(v_scales.contiguous()),
-        _ptr(out), C.byref(os_), _stream()), "attention_prefill")
+        _ptr(out), C.byref(os_), ws_ptr, ws_n, _stream()), "attention_prefill")
     return out
 
 

@@ -32,6 +32,7 @@ namespace {
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kThreads = 256;
+constexpr int kXcds = 8;  // workgroup i of a launch runs on XCD i % 8
 
 struct PrefillArgs {
     const int8_t *q, *k, *v;
@@ -44,6 +45,38 @@ struct PrefillArgs {
     int32_t q_gran, kv_gran;
     int32_t q_tiles;
     int32_t zigzag;  // pair heavy and light tiles in grids that fit at once
+};
+
+// Balanced schedule: the steps (item, key tile) of all items, items in (batch,
+// head, query tile) order and each item's tiles in key order, are cut into G
+// equal ranges, one per workgroup of the grid. An item that a range boundary
+// cuts is computed in parts; every part leaves its (running max, row sum,
+// unnormalized output) in a slot of the workspace, and the part that finishes
+// last (an item counter says which) merges the slots in part order, so the
+// result does not depend on the order the parts finish in.
+struct StreamArgs {
+    int64_t units;       // steps of all items
+    int64_t per_head;    // steps of one (batch, head)
+    uint32_t *counters;  // one per item; zero between launches (the merging part resets it)
+    float *slots;        // 2 G partial results
+};
+
+// One part of an item in the balanced schedule.
+struct StreamPart {
+    int parts;      // parts of the item (1: the whole item, no merge)
+    int slot;       // this part's slot
+    int item;       // counter index
+    int first_wg;   // logical workgroup of the item's first part
+    int self;       // this part's index among the item's parts
+    int64_t item_u0;  // first step of the item
+};
+
+enum PrefillMode { kWhole = 0, kSplit = 1, kStream = 2 };
+
+template <int D>
+struct StreamSlot {  // floats of one partial result: output in lane order, then (max, sum)
+    static constexpr int O_FLOATS = 4 * (D / 32) * 4 * kWave * 4;
+    static constexpr int FLOATS = O_FLOATS + 4 * kWave * 2;
 };
 
 // Row m of a 32-row score block holds key sigma(m) = 16 ((m >> 2) & 1) +
@@ -111,6 +144,54 @@ __device__ __forceinline__ uint32_t int8_pair_to_f16(uint32_t w0, uint32_t w1, i
 }
 #undef REEF_CVT_PAIR
 
+__device__ __forceinline__ int floor_div(int a, int b) {  // b > 0
+    return a >= 0 ? a / b : -((-a + b - 1) / b);
+}
+
+// Key tiles of query tile `tile`: the tiles from the one holding the first key
+// any row of the tile sees through the one holding the last.
+__device__ __forceinline__ int tile_steps(const PrefillArgs &a, int tile, int &kt_first) {
+    const int q0 = tile * kBM;
+    const int r_last = min(q0 + kBM, a.q_len) - 1;
+    const int key_lo = a.window > 0 ? max(0, a.query_start + q0 + 1 - a.window) : 0;
+    const int key_hi = min(a.query_start + r_last, a.kv_len - 1);
+    kt_first = key_lo / kBN * kBN;
+    return (key_hi - kt_first) / kBN + 1;
+}
+
+// Sum of tile_steps over the query tiles t < T, for T < q_tiles (every such tile
+// is full). With query_start + q_len <= kv_len the last key of tile t is
+// query_start + 128 t + 127, in tile 2 t + (query_start + 127) / 64; with a window
+// the first is max(0, query_start + 128 t + 1 - window), in tile
+// 2 t + floor((query_start + 1 - window) / 64) once t reaches t0.
+__device__ __forceinline__ int64_t steps_before(const PrefillArgs &a, int T) {
+    const int64_t t = T;
+    int64_t s = t + t * (t - 1) + (int64_t)((a.query_start + 127) / 64) * t;
+    if (a.window > 0) {
+        const int t0 = max(0, floor_div(a.window - a.query_start - 1, kBM) + 1);
+        if (T > t0)
+            s -= (t - t0) * (t + t0 - 1) +
+                 (int64_t)floor_div(a.query_start + 1 - a.window, kBN) * (t - t0);
+    }
+    return s;
+}
+
+// The balanced schedule visits a head's query tiles heaviest and lightest in
+// turn: z = 0, 1, 2, 3, ... is tile Q - 1, 0, Q - 2, 1, ..., so that the steps
+// of neighbouring tiles add up to about the same, and a workgroup's range holds
+// one or two parts of items rather than several light items.
+__device__ __forceinline__ int zigzag_tile(int q_tiles, int z) {
+    return (z & 1) ? z >> 1 : q_tiles - 1 - (z >> 1);
+}
+
+// Steps of the first Z tiles of a head in that order (Z < q_tiles): the Z/2
+// lightest and the Z - Z/2 heaviest.
+__device__ __forceinline__ int64_t steps_before_zigzag(const PrefillArgs &a, int64_t per_head,
+                                                       int Z) {
+    if (Z == 0) return 0;
+    return per_head - steps_before(a, a.q_tiles - (Z + 1) / 2) + steps_before(a, Z / 2);
+}
+
 // Work items are (query tile, batch x head), ranked heaviest first: the causal
 // rows of the last tile see the most keys.
 __device__ __forceinline__ void item_coords(const PrefillArgs &a, int rank, int &tile, int &b,
@@ -149,10 +230,17 @@ struct PrefillLds {
 // with its own LDS stages, and group 0 merges both partial results at the end.
 // This halves the longest sequential chain of a workgroup, which balances causal
 // grids that fit the GPU at once.
-template <int D, bool KV_TOKEN, bool PRECISE, bool SPLIT>
-__device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int8_t *smem_all,
-                                             float (*sScale)[KV_TOKEN ? 2 * kBN + 1 : 1]) {
-    static_assert(!SPLIT || !KV_TOKEN, "the split kernel has no per-token K/V scales");
+//
+// MODE kWhole and kStream compute key tiles [c0, c1) of the item (kWhole: all of
+// them); kStream parts of a cut item merge through the workspace (StreamArgs).
+template <int D, bool KV_TOKEN, bool PRECISE, int MODE>
+__device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int b, int h, int c0,
+                                             int c1, int8_t *smem_all,
+                                             float (*sScale)[KV_TOKEN ? 2 * kBN + 1 : 1],
+                                             const StreamArgs &sa, const StreamPart &sp,
+                                             uint32_t *sTicket) {
+    constexpr bool SPLIT = MODE == kSplit;
+    static_assert(MODE == kWhole || !KV_TOKEN, "only whole items have per-token K/V scales");
     constexpr int KSTRIDE = PrefillLds<D>::KSTRIDE, VSTRIDE = PrefillLds<D>::VSTRIDE;
     constexpr int DB = D / 32;  // 32-wide output blocks
     constexpr int K_BYTES = PrefillLds<D>::K_BYTES, V_BYTES = PrefillLds<D>::V_BYTES;
@@ -167,8 +255,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int
     const int group = SPLIT ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) : 0;
     int8_t *smem = smem_all + group * PrefillLds<D>::BYTES;
     const int col = lane & 31, grp = lane >> 5;
-    int tile, b, h;
-    item_coords(a, rank, tile, b, h);
     const int kvh = h / (a.q_heads / a.kv_heads);
     const int q0 = tile * kBM;
     const int row = q0 + wave * 32 + col;
@@ -277,9 +363,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int
     const int kt_first = key_lo / kBN * kBN;
     const int n_all = (key_hi - kt_first) / kBN + 1;
     // This group's tiles: [kt0, kt0 + n_tiles * kBN); both groups run n_iter steps.
-    const int n_iter = SPLIT ? (n_all + 1) / 2 : n_all;
-    const int kt0 = kt_first + (group ? n_iter * kBN : 0);
-    const int n_tiles = group ? n_all - n_iter : n_iter;
+    int n_iter, kt0, n_tiles;
+    if (SPLIT) {
+        n_iter = (n_all + 1) / 2;
+        kt0 = kt_first + (group ? n_iter * kBN : 0);
+        n_tiles = group ? n_all - n_iter : n_iter;
+    } else {
+        kt0 = kt_first + c0 * kBN;
+        n_tiles = min(c1, n_all) - c0;
+        n_iter = n_tiles;
+    }
     if (n_tiles > 0) load_tile(kt0);
     i32x4 qop[D / 32];
     load_q_operand<D>(qop, a.q + b * a.q_sb + h * a.q_sh + (int64_t)(row_ok ? row : 0) * a.q_st,
@@ -502,6 +595,94 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int rank, int
                 for (int i = 0; i < 4; ++i) acc[d][4 * j + i] = acc[d][4 * j + i] * w0 + o[i] * w1;
             }
     }
+    if (MODE == kStream && sp.parts > 1) {
+        // Leave this part in its slot (every lane: rows past q_len hold finite
+        // values), then count the part in; the last part of the item merges. The
+        // slot stores and loads and the counter are device-coherent accesses of
+        // their own (sc1), so no L2 write-back or invalidation is needed: the
+        // stores complete (vmcnt 0) before the workgroup's count.
+        constexpr int SF = StreamSlot<D>::FLOATS, OF = StreamSlot<D>::O_FLOATS;
+        constexpr int E = DB * 8;  // 8-byte elements of output per lane
+        auto pack = [](float x, float y) {
+            return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+        };
+        auto put = [](uint64_t *p, uint64_t v) {
+            __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        };
+        auto get = [](const uint64_t *p) {
+            return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        };
+        // Element e of wave w, lane l at [(w E + e) 64 + l]: each store is 512
+        // contiguous bytes.
+        uint64_t *so = reinterpret_cast<uint64_t *>(sa.slots + (int64_t)sp.slot * SF);
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                put(so + (wave * E + d * 8 + e) * kWave + lane,
+                    pack(acc[d][2 * e], acc[d][2 * e + 1]));
+        put(so + OF / 2 + wave * kWave + lane, pack(m_run, l_tot));
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            *sTicket = __hip_atomic_fetch_add(sa.counters + sp.item, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*sTicket != (uint32_t)(sp.parts - 1)) return;
+        if (tid == 0)  // ready for the next launch
+            __hip_atomic_store(sa.counters + sp.item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Parts in order: part p is workgroup first_wg + p; the first part sits in
+        // its workgroup's second slot when that range began before the item.
+        auto slot_of = [&](int p) {
+            const int L = sp.first_wg + p;
+            const bool second = p == 0 && (int64_t)L * sa.units / gridDim.x < sp.item_u0;
+            return reinterpret_cast<const uint64_t *>(sa.slots +
+                                                      (int64_t)(2 * L + (second ? 1 : 0)) * SF);
+        };
+        // This part comes from registers, the others from their slots, summed in
+        // part order either way with explicit fused multiply-adds (the same
+        // roundings whichever part merges).
+        float m = m_run;
+        for (int p = 0; p < sp.parts; ++p)
+            if (p != sp.self)
+                m = fmaxf(m, __uint_as_float((uint32_t)get(slot_of(p) + OF / 2 + wave * kWave + lane)));
+        float l = 0.0f;
+        f32x16 tot[DB];
+#pragma unroll
+        for (int d = 0; d < DB; ++d) tot[d] = f32x16{};
+        for (int p = 0; p < sp.parts; ++p) {
+            if (p == sp.self) {
+                const float w = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+                l = __builtin_fmaf(w, l_tot, l);
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) tot[d][i] = __builtin_fmaf(w, acc[d][i], tot[d][i]);
+                continue;
+            }
+            const uint64_t *sl = slot_of(p);
+            const uint64_t ml = get(sl + OF / 2 + wave * kWave + lane);
+            uint64_t v[DB * 8];
+#pragma unroll
+            for (int e = 0; e < DB * 8; ++e) v[e] = get(sl + (wave * E + e) * kWave + lane);
+            const float mp = __uint_as_float((uint32_t)ml), lp = __uint_as_float((uint32_t)(ml >> 32));
+            const float w = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - m);
+            l = __builtin_fmaf(w, lp, l);
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    tot[d][2 * e] =
+                        __builtin_fmaf(w, __uint_as_float((uint32_t)v[d * 8 + e]), tot[d][2 * e]);
+                    tot[d][2 * e + 1] = __builtin_fmaf(
+                        w, __uint_as_float((uint32_t)(v[d * 8 + e] >> 32)), tot[d][2 * e + 1]);
+                }
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) acc[d] = tot[d];
+        l_tot = l;
+    }
     if (!row_ok) return;
     const float norm = (KV_TOKEN ? s_run : cv) / l_tot;
     float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
@@ -535,7 +716,10 @@ __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillA
             if (r * G >= items) break;
             continue;  // a reversed last round with fewer items than workgroups
         }
-        prefill_body<D, false, false, true>(a, item, smem, sScale);
+        int tile, b, h;
+        item_coords(a, item, tile, b, h);
+        prefill_body<D, false, false, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
+                                              StreamPart{}, nullptr);
         __syncthreads();  // the next item's stages overwrite the merge buffer
     }
 }
@@ -544,7 +728,65 @@ template <int D, bool KV_TOKEN, bool PRECISE>
 __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
-    prefill_body<D, KV_TOKEN, PRECISE, false>(a, grid_rank(a), smem, sScale);
+    int tile, b, h;
+    item_coords(a, grid_rank(a), tile, b, h);
+    prefill_body<D, KV_TOKEN, PRECISE, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
+                                               StreamArgs{}, StreamPart{}, nullptr);
+}
+
+// Balanced schedule (StreamArgs): workgroup g works through the steps
+// [L G^-1 units, (L + 1) G^-1 units) of logical workgroup L, where the G / 8
+// workgroups that run on one XCD (hardware workgroup g goes to XCD g % 8) hold
+// consecutive L, so an XCD's L2 sees a few heads, not all of them.
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void prefill_stream_kernel(PrefillArgs a, StreamArgs sa) {
+    __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
+    __shared__ float sScale[2][1];
+    __shared__ uint32_t sTicket;
+    const int G = gridDim.x, g = blockIdx.x;
+    const int x = g % kXcds, per = G / kXcds, rem = G % kXcds;
+    const int L = x * per + min(x, rem) + g / kXcds;
+    int64_t u = (int64_t)L * sa.units / G;
+    const int64_t u_end = (int64_t)(L + 1) * sa.units / G;
+    // Locate the first step (the grid has at most one workgroup per step, so the
+    // range is not empty): (batch, head), then the tile's place in the head's
+    // order by bisection over the closed-form prefix sums.
+    int bh = (int)(u / sa.per_head);
+    int64_t r = u - (int64_t)bh * sa.per_head;
+    int lo = 0, hi = a.q_tiles - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (steps_before_zigzag(a, sa.per_head, mid) <= r) lo = mid;
+        else hi = mid - 1;
+    }
+    int z = lo;
+    int c0 = (int)(r - steps_before_zigzag(a, sa.per_head, z));
+    const int64_t W = sa.units;
+    auto wg_of = [&](int64_t unit) { return (int)(((unit + 1) * G - 1) / W); };
+    bool first = true;
+    while (u < u_end) {
+        const int tile = zigzag_tile(a.q_tiles, z);
+        int kt_first;
+        const int n = tile_steps(a, tile, kt_first);
+        const int c1 = (int)(c0 + (u_end - u) < n ? c0 + (u_end - u) : n);
+        StreamPart sp;
+        sp.item_u0 = u - c0;
+        sp.first_wg = wg_of(sp.item_u0);
+        sp.parts = wg_of(sp.item_u0 + n - 1) - sp.first_wg + 1;
+        sp.slot = 2 * L + (first ? 0 : 1);
+        sp.self = L - sp.first_wg;
+        sp.item = bh * a.q_tiles + tile;
+        prefill_body<D, false, false, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0, c1,
+                                               smem, sScale, sa, sp, &sTicket);
+        u += c1 - c0;
+        c0 = 0;
+        first = false;
+        if (++z == a.q_tiles) {
+            z = 0;
+            ++bh;
+        }
+        __syncthreads();  // the next item's first stage reuses the LDS
+    }
 }
 
 // Bit-exact hook: the int32 score accumulators, through score_tile. One wave
@@ -597,16 +839,70 @@ bool valid_granularity(int32_t g) {
     return g == REEF_SCALE_PER_TENSOR || g == REEF_SCALE_PER_HEAD || g == REEF_SCALE_PER_TOKEN;
 }
 
+int64_t floor_div_host(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+
+// Host copies of tile_steps / steps_before (query tiles of 128 rows, key tiles of 64).
+int64_t host_tile_steps(const reef_attention_params &p, int64_t tile) {
+    const int64_t q0 = tile * kBM, r_last = std::min(q0 + kBM, p.q_len) - 1;
+    const int64_t key_lo = p.window > 0 ? std::max<int64_t>(0, p.query_start + q0 + 1 - p.window) : 0;
+    const int64_t key_hi = std::min(p.query_start + r_last, p.kv_len - 1);
+    const int64_t kt_first = key_lo / kBN * kBN;
+    return (key_hi - kt_first) / kBN + 1;
+}
+
+int64_t host_steps_before(const reef_attention_params &p, int64_t t) {
+    int64_t s = t + t * (t - 1) + ((p.query_start + 127) / 64) * t;
+    if (p.window > 0) {
+        const int64_t t0 = std::max<int64_t>(0, floor_div_host(p.window - p.query_start - 1, kBM) + 1);
+        if (t > t0)
+            s -= (t - t0) * (t + t0 - 1) + floor_div_host(p.query_start + 1 - p.window, kBN) * (t - t0);
+    }
+    return s;
+}
+
+// The balanced schedule's grid: two 4-wave workgroups per compute unit.
+int64_t stream_groups() { return 2 * compute_units(); }
+
+int64_t stream_counter_bytes(const reef_attention_params &p) {
+    const int64_t items = ceil_div(p.q_len, kBM) * p.q_heads * p.batch;
+    return ceil_div(items * 4, 256) * 256;
+}
+
+int64_t stream_slot_floats(int64_t D) {
+    return D == 128 ? StreamSlot<128>::FLOATS : StreamSlot<64>::FLOATS;
+}
+
+// Items of a launch at or below which the balanced schedule is used. With one
+// item per compute unit or fewer, a causal grid leaves most units idle for most
+// of the launch, and cutting items pays; from two items per compute unit the
+// one-item grid pairs a heavy and a light item on each unit instead, and the
+// cuts' partial results (written, counted in, merged: about 5 us per cut item)
+// cost more than the balance gains (measured on 1x32x2048x128: 60 us balanced,
+// 49 us paired).
+int64_t stream_item_limit() {
+    const char *e = getenv("REEF_PREFILL_STREAM_ITEMS");
+    return e ? atoll(e) : compute_units();
+}
+
 }  // namespace
 }  // namespace reef
 
 using namespace reef;
 
+extern "C" size_t reef_attention_prefill_workspace_bytes(const reef_attention_params *p) {
+    if (!p || p->batch <= 0 || p->q_heads <= 0 || p->q_len <= 0 ||
+        (p->head_dim != 64 && p->head_dim != 128))
+        return 0;
+    return (size_t)(stream_counter_bytes(*p) +
+                    2 * stream_groups() * stream_slot_floats(p->head_dim) * 4);
+}
+
 extern "C" reef_status reef_attention_prefill_int8(
     const reef_attention_params *p, const int8_t *q, const reef_strides *q_strides,
     const int8_t *k, const reef_strides *k_strides, const int8_t *v, const reef_strides *v_strides,
     const float *q_scales, const float *k_scales, const float *v_scales, float *out,
-    const reef_strides *out_strides, hipStream_t stream) {
+    const reef_strides *out_strides, void *workspace, size_t workspace_bytes,
+    hipStream_t stream) {
     if (!p || !q || !k || !v || !q_scales || !k_scales || !v_scales || !out)
         return REEF_INVALID_ARGUMENT;
     const int64_t D = p->head_dim;
@@ -677,6 +973,28 @@ extern "C" reef_status reef_attention_prefill_int8(
     // kernel is the only parallelism left to balance the causal work; with more,
     // two one-item workgroups per compute unit overlap each other's prologue and
     // epilogue better.
+    // The balanced schedule needs the caller's workspace; without it, small grids
+    // take the persistent split kernel.
+    if (workspace && !aligned(workspace, 256)) return REEF_INVALID_ARGUMENT;
+    const bool stream_ok = workspace && workspace_bytes >= reef_attention_prefill_workspace_bytes(p);
+    if (!tok && !precise && stream_ok && items <= stream_item_limit()) {
+        const int64_t per_head = host_steps_before(*p, a.q_tiles - 1) +
+                                 host_tile_steps(*p, a.q_tiles - 1);
+        StreamArgs sa;
+        sa.per_head = per_head;
+        sa.units = per_head * p->batch * Hq;
+        sa.counters = static_cast<uint32_t *>(workspace);
+        sa.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + stream_counter_bytes(*p));
+        if (sa.units >= (int64_t(1) << 40)) return REEF_UNSUPPORTED;
+        // No more workgroups than steps: every range holds at least one step, so the
+        // workgroups between an item's first and last part each hold a part of it.
+        const dim3 sgrid((unsigned)std::min<int64_t>(stream_groups(), sa.units));
+        if (D == 128)
+            hipLaunchKernelGGL(prefill_stream_kernel<128>, sgrid, dim3(kThreads), 0, stream, a, sa);
+        else
+            hipLaunchKernelGGL(prefill_stream_kernel<64>, sgrid, dim3(kThreads), 0, stream, a, sa);
+        return launch_status();
+    }
     const char *sp = getenv("REEF_PREFILL_SPLIT");
     const bool split =
         !tok && !precise && (sp ? atoi(sp) != 0 : items <= compute_units());

@@ -38,7 +38,8 @@ def _prefill(p, strides=None):
     lib = reef_amd.lib()
     s = C.byref(strides) if strides else None
     return lib.reef_attention_prefill_int8(C.byref(p), _fake(1), s, _fake(2), s, _fake(3), s,
-                                           _fake(4), _fake(5), _fake(6), _fake(7), None, None)
+                                           _fake(4), _fake(5), _fake(6), _fake(7), None, None, 0,
+                                           None)
 
 
 def good_params(**kw):
@@ -66,8 +67,23 @@ def test_prefill_rejects_null_and_misaligned():
     lib = reef_amd.lib()
     p = good_params()
     assert lib.reef_attention_prefill_int8(C.byref(p), None, None, None, None, None, None, None,
-                                           None, None, None, None, None) == 1
+                                           None, None, None, None, None, 0, None) == 1
     assert _prefill(p, Strides(0, 128, 129)) == reef_amd.INVALID_ARGUMENT  # row not 16-B aligned
+
+
+def test_prefill_workspace_bytes_and_alignment():
+    lib = reef_amd.lib()
+    p = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048)
+    n = lib.reef_attention_prefill_workspace_bytes(C.byref(p))
+    # item counters (512 items), then two partial slots per workgroup, two workgroups per
+    # compute unit (256 without a GPU): 128 x 128 outputs plus (max, sum) of 128 rows
+    assert n == 2048 + 2 * 512 * (128 * 128 + 2 * 256) * 4
+    assert lib.reef_attention_prefill_workspace_bytes(C.byref(good_params(head_dim=96))) == 0
+    assert lib.reef_attention_prefill_workspace_bytes(None) == 0
+    # a workspace that is not 256-byte aligned
+    assert lib.reef_attention_prefill_int8(C.byref(p), _fake(1), None, _fake(2), None, _fake(3),
+                                           None, _fake(4), _fake(5), _fake(6), _fake(7), None,
+                                           C.c_void_p(0x10010), n, None) == reef_amd.INVALID_ARGUMENT
 
 
 def test_decode_host_validation_and_workspace():

@@ -153,14 +153,15 @@ def _quantize(x, gran):
     return oracle.quantize_per_token(x)
 
 
-def _run_prefill(reef, q, k, v, p, precise=False):
+def _run_prefill(reef, q, k, v, p, precise=False, workspace=None):
     qq, qs = _quantize(q, p.q_granularity)
     kq, ks = _quantize(k, p.kv_granularity)
     vq, vs = _quantize(v, p.kv_granularity)
     out = reef.attention_prefill(gpu(qq), gpu(kq), gpu(vq), gpu(qs), gpu(ks), gpu(vs),
                                  query_start=p.start(), window=p.window,
                                  softmax_scale=p.softmax_scale, q_granularity=p.q_granularity,
-                                 kv_granularity=p.kv_granularity, precise=precise)
+                                 kv_granularity=p.kv_granularity, precise=precise,
+                                 workspace=workspace)
     gold = oracle.attention_int8(p, qq, kq, vq, qs, ks, vs)
     return host(out), gold
 
@@ -211,17 +212,64 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
     p = oracle.Problem(B, Hq, Hkv, Sq, Skv, D, query_start=start, window=window,
                        softmax_scale=(1 / math.sqrt(D)) if scale is None else scale,
                        q_granularity=gq, kv_granularity=gkv)
-    # both fp16 P and split P; the one-item-per-workgroup and the persistent
-    # key-split kernels (chosen by size, forced here through REEF_PREFILL_SPLIT)
-    for precise, split in ((False, "0"), (False, "1"), (True, "0")):
+    # both fp16 P and split P; the balanced schedule (with a workspace), and without
+    # one the one-item-per-workgroup and the persistent key-split kernels (chosen by
+    # size, forced here through REEF_PREFILL_SPLIT)
+    for precise, split, ws in ((False, "0", None), (False, "0", False), (False, "1", False),
+                               (True, "0", None)):
         os.environ["REEF_PREFILL_SPLIT"] = split
         try:
-            out, gold = _run_prefill(reef, q, k, v, p, precise)
+            out, gold = _run_prefill(reef, q, k, v, p, precise, workspace=ws)
         finally:
             del os.environ["REEF_PREFILL_SPLIT"]
         err = np.abs(out - gold).max()
-        print(f"precise={precise} split={split} max_abs_err {err:.3e}", flush=True)
-        assert err <= TOL, (precise, split, err)
+        print(f"precise={precise} split={split} workspace={ws is not False} "
+              f"max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL, (precise, split, ws, err)
+
+
+STREAM_CASES = [
+    # B, Hq, Hkv, Sq, Skv, D, query_start, window, gran
+    (1, 1, 1, 2048, 2048, 128, None, 0, 1),    # 272 steps for 512 workgroups: up to 32 parts
+    (1, 4, 1, 4096, 4096, 128, None, 0, 1),    # GQA, the last items in 3 parts
+    (2, 3, 1, 1000, 1500, 64, None, 300, 0),   # window, query_start 500, ragged last tile
+    (1, 2, 2, 700, 900, 128, 150, 0, 1),       # explicit start below kv_len - q_len
+    (3, 16, 4, 384, 384, 64, None, 0, 1),      # whole items between cut ones
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D,start,window,gran", STREAM_CASES)
+def test_prefill_balanced_schedule(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gran):
+    """The balanced schedule cuts items at workgroup boundaries and merges their
+    parts through the workspace: same tolerance, bit-identical on a second call
+    (the merge order is fixed), and the item counters back at zero."""
+    case(f"prefill balanced B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} start{start} "
+         f"win{window} gran{gran}")
+    seed = 5 * B + Sq + 2 * Skv + D
+    q = W.lcg_normal(seed, B * Hq * Sq * D).reshape(B, Hq, Sq, D)
+    k = W.lcg_normal(seed + 1, B * Hkv * Skv * D).reshape(B, Hkv, Skv, D)
+    v = W.lcg_normal(seed + 2, B * Hkv * Skv * D).reshape(B, Hkv, Skv, D)
+    p = oracle.Problem(B, Hq, Hkv, Sq, Skv, D, query_start=start, window=window,
+                       softmax_scale=1 / math.sqrt(D), q_granularity=gran, kv_granularity=gran)
+    qq, qs = _quantize(q, gran)
+    kq, ks = _quantize(k, gran)
+    vq, vs = _quantize(v, gran)
+    gold = oracle.attention_int8(p, qq, kq, vq, qs, ks, vs)
+    params = reef.AttentionParams(B, Hq, Hkv, Sq, Skv, D, p.start(), window, p.softmax_scale,
+                                  gran, gran, 0)
+    n = reef.lib().reef_attention_prefill_workspace_bytes(reef.C.byref(params))
+    ws = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    args = (gpu(qq), gpu(kq), gpu(vq), gpu(qs), gpu(ks), gpu(vs))
+    kw = dict(query_start=p.start(), window=window, softmax_scale=p.softmax_scale,
+              q_granularity=gran, kv_granularity=gran, workspace=ws)
+    out1 = host(reef.attention_prefill(*args, **kw))
+    out2 = host(reef.attention_prefill(*args, **kw))
+    err = np.abs(out1 - gold).max()
+    print(f"max_abs_err {err:.3e}", flush=True)
+    assert err <= TOL
+    assert np.array_equal(out1, out2)
+    items = B * Hq * ((Sq + 127) // 128)
+    assert not host(ws[:4 * items]).any()
 
 
 @pytest.mark.parametrize("D", [64, 128])
