@@ -523,9 +523,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             }
             };
 
-    // One pipeline step: the next tile's loads in flight during this tile's math,
-    // then its LDS stores. With `every_row` the tile is inside the visible range of
-    // every row of the workgroup, so no wave skips it or masks it: such steps run in
+    // One pipeline step: this tile's math while the next tile's loads (issued at the
+    // end of the previous step) are in flight, then its LDS stores. With
+    // `every_row` the tile is inside the visible range of every row of the
+    // workgroup, so no wave skips it or masks it: such steps run in
     // a loop of their own with a single code path, which keeps the output
     // accumulators in place (merging the masked and unmasked versions of a tile
     // would copy all of them on every step).
@@ -533,7 +534,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
         constexpr bool every_row = decltype(every_row_tag)::value;
         const int kt = kt0 + it * kBN;
         const int buf = it & 1;
-        if (it + 1 < n_tiles) load_tile(kt + kBN);
         if constexpr (every_row) {
             tile_math(kt, buf, std::false_type{});
         } else {
@@ -547,6 +547,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             }
         }
         if (it + 1 < n_tiles) store_tile(buf ^ 1);
+        // The registers are free again: the loads of the tile after next fly through
+        // the barrier and the whole next step.
+        if (it + 2 < n_tiles) load_tile(kt + 2 * kBN);
         __syncthreads();
     };
     // Steps [it_a, it_b): tiles every row of the workgroup sees whole. Rows past
@@ -558,6 +561,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kBN : 0));
 
     if (n_tiles > 0) store_tile(0);
+    if (n_tiles > 1) load_tile(kt0 + kBN);
     __syncthreads();
     int it = 0;
     for (; it < it_a; ++it) step(it, std::false_type{});
