@@ -202,7 +202,7 @@ reef_status reef_attention_int8_integer(const reef_attention_params *p, const in
 
 /* ---------------------------------------------------------------------------
  * Decode over an int8 KV cache (one query token per sequence), split across
- * workgroups along the keys, partial results combined by log-sum-exp.
+ * waves along the keys, partial results combined by log-sum-exp.
  *
  * KV cache format (int8 values, fp32 per-token-per-head scales). The cache is
  * cut into pages of 16 tokens. A K page is [16, D] (token-major, like the
@@ -233,7 +233,12 @@ typedef struct reef_decode_params {
     uint32_t flags;
 } reef_decode_params;
 
-/* Bytes of device workspace the decode entry points need for params. */
+/* Bytes of device workspace the decode entry points need for params: one
+ * counter per (sequence, kv head) and, when a sequence's keys are split over
+ * more than one workgroup, one partial result per workgroup, merged by the last
+ * workgroup of the sequence inside the same launch. The workspace must be
+ * zero-filled before its first use; every call leaves it ready for the next
+ * (no refill). Calls that may run at the same time need separate workspaces. */
 size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p);
 
 reef_status reef_attention_decode_int8(const reef_decode_params *p, const int8_t *q,

@@ -164,6 +164,7 @@ void check_context_and_decode(std::mt19937 &g, int64_t window) {
     reef_decode_params dp{1, (int64_t)H, (int64_t)H, (int64_t)D, (int64_t)L, window, 1.0f,
                           REEF_SCALE_PER_TOKEN, 0, 0};
     Dev<std::uint8_t> ws(reef_hip::decode_workspace_bytes(dp));
+    if (hipMemset(ws.p, 0, ws.n) != hipSuccess) throw std::runtime_error("hipMemset");  // once
     reef_hip::decode(dp, dql.p, dqls.p, kc.p, vc.p, kcs.p, vcs.p, lens.p, dlast.p, ws.p, ws.n,
                      status.p, nullptr);
     reef_hip::check_status_word(status.p, nullptr, "decode");

@@ -348,9 +348,11 @@ def _decode_params(q, max_context, kv_heads, window, softmax_scale, q_granularit
 
 
 def decode_workspace(params: DecodeParams, device):
+    """A zero-filled decode workspace (its item counters must start at zero; every
+    launch leaves them so, so the workspace is reusable without refilling)."""
     torch = _torch()
     n = lib().reef_attention_decode_workspace_bytes(C.byref(params))
-    return torch.empty(max(n, 16) // 4 + 4, dtype=torch.float32, device=device)
+    return torch.zeros(max(n, 16) // 4 + 4, dtype=torch.float32, device=device)
 
 
 def attention_decode(q, q_scales, k_cache, v_pages, k_scales, v_scales, context_lens=None, *,

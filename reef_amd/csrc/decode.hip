@@ -41,8 +41,8 @@ struct DecodeArgs {
     const float *ks, *vs;
     const int32_t *block_table;  // paged only
     const int32_t *context_lens; // may be null
-    float *part_o;          // [B, Hq, splits, D]
-    float *part_ml;         // [B, Hq, splits, 2] (max in log2 units, sum)
+    uint32_t *counters;     // one per (sequence, kv head); zero between launches
+    float *slots;           // [B * Hkv, groups] parts (DecodeSlot), with groups > 1
     uint32_t *status;
     int32_t batch, q_heads, kv_heads, group;
     int32_t max_context, window, splits;
@@ -52,9 +52,18 @@ struct DecodeArgs {
     float score_scale;  // softmax_scale * log2(e)
 };
 
-// Addresses of one 16-token page of (sequence b, kv head kvh). Pages at or past
-// n_pages (the sequence's ceil(len / 16)) are never looked up: they point at a
-// safe page and are dead. A page number outside [0, num_pages) is an error.
+// Page number of page_idx of sequence b from the block table (paged only), read
+// ahead of the page's data: pages at or past n_pages (the sequence's
+// ceil(len / 16)) are not looked up.
+template <bool PAGED>
+__device__ __forceinline__ int table_page(const DecodeArgs &a, int b, int page_idx, int n_pages) {
+    if (!PAGED || page_idx >= n_pages) return 0;
+    return a.block_table[(int64_t)b * a.max_blocks + page_idx];
+}
+
+// Addresses of one 16-token page of (sequence b, kv head kvh), `page` its number
+// from table_page. Pages at or past n_pages point at a safe page and are dead. A
+// page number outside [0, num_pages) is an error.
 struct PageRef {
     const int8_t *k;   // [16, D]
     const int8_t *vt;  // [D, 16]
@@ -65,11 +74,10 @@ struct PageRef {
 
 template <int D, bool PAGED>
 __device__ __forceinline__ PageRef page_ref(const DecodeArgs &a, int b, int kvh, int page_idx,
-                                            int n_pages) {
+                                            int n_pages, int page) {
     PageRef r;
     const bool in_seq = page_idx < n_pages;
     if (PAGED) {
-        int page = in_seq ? a.block_table[(int64_t)b * a.max_blocks + page_idx] : 0;
         const bool valid = page >= 0 && page < a.num_pages;
         r.ok = valid || !in_seq;
         r.live = in_seq && valid;
@@ -120,9 +128,221 @@ __device__ __forceinline__ i32x4 load_stream(const i32x4 *p) {
     return NT ? __builtin_nontemporal_load(p) : *p;
 }
 
+// One 64-key block in registers: the operands of both matrix products and,
+// per lane, the K and V scale of key 16 grp + col (the 16 lanes of a group
+// hold the 16 scales of its page, handed around with shuffles).
+template <int D>
+struct DecodeBlock {
+    i32x4 k[4][D / 64];
+    i32x4 v[D / 16];
+    float ks, vs;
+    bool live;
+};
+
+// A wave's running state over its keys: max (log2 units), row sum, the value
+// normalizer s_run and the accumulator in units of s_run.
+template <int D>
+struct DecodeRun {
+    float m_run, l_run, s_run, inv_s;
+    f32x4 acc[D / 16];
+};
+
+// 8-byte elements of one workgroup's part in the workspace: the output in
+// [element][lane] order, then (max, sum).
+template <int D>
+struct DecodeSlot {
+    static constexpr int O = 2 * (D / 16);
+    static constexpr int ELEMS = (O + 1) * kWave;
+};
+
+template <int D>
+__device__ __forceinline__ void reset_run(DecodeRun<D> &r) {
+    r.m_run = -INFINITY;
+    r.l_run = 0.0f;
+    r.s_run = 0.0f;
+    r.inv_s = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D / 16; ++d) r.acc[d] = f32x4{};
+}
+
+// Block-table entries of the block at key kb, read one block ahead of the
+// block's data so that the data loads never wait on a table load: lane l holds
+// entry l % 4 of the block's 4 pages, handed to the lanes that need it.
+template <bool PAGED>
+__device__ __forceinline__ int fetch_pages(const DecodeArgs &a, int b, int kb, int n_pages, int lane) {
+    return table_page<PAGED>(a, b, kb / kPage + (lane & 3), n_pages);
+}
+
+// Issues the loads of the block at key kb (pages: from fetch_pages).
 template <int D, bool PAGED>
-__global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs a) {
-    constexpr int KS = D / 64;   // 64-wide reduction steps of the score instruction
+__device__ __forceinline__ void load_block(const DecodeArgs &a, int b, int kvh, int kb, int n_pages,
+                                           int pages, int col, int grp, DecodeBlock<D> &x,
+                                           bool &bad_page) {
+    constexpr int KS = D / 64, DB = D / 16;
+    const int page0 = kb / kPage;
+    // K rows for the score instruction: row m = col of block t is key
+    // 16 (m / 4) + 4t + (m % 4), in page m / 4.
+    const PageRef kp = page_ref<D, PAGED>(a, b, kvh, page0 + (col >> 2), n_pages,
+                                          PAGED ? __shfl(pages, col >> 2) : 0);
+    // This lane group's page for scales, P and V.
+    const PageRef gp = page_ref<D, PAGED>(a, b, kvh, page0 + grp, n_pages,
+                                          PAGED ? __shfl(pages, grp) : 0);
+    bad_page |= !gp.ok;
+    x.live = gp.live;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            x.k[t][s] = load_stream<!PAGED>(reinterpret_cast<const i32x4 *>(
+                kp.k + (4 * t + (col & 3)) * D + 64 * s + 16 * grp));
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+        x.v[d] = load_stream<!PAGED>(reinterpret_cast<const i32x4 *>(gp.vt + (16 * d + col) * kPage));
+    x.ks = gp.ks[col];
+    x.vs = gp.vs[col];
+}
+
+// Scores, online softmax and P.V of one block for keys [lo, k_end).
+template <int D>
+__device__ __forceinline__ void block_math(const DecodeBlock<D> &cur, int kb, int lo, int k_end,
+                                           const i32x4 (&qop)[D / 64], float c, int lane,
+                                           DecodeRun<D> &st) {
+    constexpr int KS = D / 64, DB = D / 16;
+    const int grp = lane >> 4;
+    const auto &kop = cur.k;
+    const auto &vop = cur.v;
+    const int row0 = lane & ~15;  // first lane of this lane group
+    float ksc[16], vsc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        ksc[r] = __shfl(cur.ks, row0 + r);
+        vsc[r] = __shfl(cur.vs, row0 + r);
+    }
+    const bool live_g = cur.live;
+
+    float x[16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        i32x4 s = {0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s = mfma_16x16x64_i8(kop[t][ks], qop[ks], s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * t + i] = (float)s[i] * (c * ksc[4 * t + i]);
+    }
+    // Blocks wholly inside [lo, k_end) on live pages skip the masks. In the
+    // others, keys outside or on a dead page take no part: score -inf and
+    // value scale 0 (the cache past a sequence's end may hold anything).
+    const bool full = kb >= lo && kb + kBlockKeys <= k_end && __all(live_g);
+    float vv[16];
+    if (full) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) vv[r] = vsc[r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kb + 16 * grp + r;
+            const bool vis = key >= lo && key < k_end && live_g;
+            if (!vis) x[r] = -INFINITY;
+            vv[r] = vis ? vsc[r] : 0.0f;
+        }
+    }
+    float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    float vmax = fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3]));
+#pragma unroll
+    for (int r = 4; r < 16; r += 2) {
+        mt = fmaxf(mt, fmaxf(x[r], x[r + 1]));
+        vmax = fmaxf(vmax, fmaxf(vv[r], vv[r + 1]));
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+
+    // Lazy rescale: the running max moves only when a head's block max exceeds
+    // it by more than 2^8, and the value normalizer s_run (values accumulate in
+    // units of s_run, the largest value scale so far) only when a value scale
+    // exceeds it 16-fold, so p * v_scale / s_run stays below 2^12 in fp16.
+    if (__any(mt > st.m_run + 8.0f || vmax > st.s_run * 16.0f)) {
+        const float m_new = fmaxf(st.m_run, mt);
+        const float s_new = fmaxf(st.s_run, vmax);
+        const float alpha = st.m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m_run - m_new);
+        const float alpha_o = s_new > 0.0f ? alpha * (st.s_run / s_new) : alpha;
+        st.inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
+        st.m_run = m_new;
+        st.s_run = s_new;
+        st.l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) st.acc[d] *= alpha_o;
+    }
+    const float m_use = st.m_run == -INFINITY ? 0.0f : st.m_run;
+
+    // P operand: lane group g's keys 16g + 8h + e for the two halves h.
+    f16x8 pop[2];
+    float lp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(x[r] - m_use);
+        lp[r & 3] += p;
+        pop[r >> 3][r & 7] = (_Float16)(p * (vv[r] * st.inv_s));
+    }
+    st.l_run += (lp[0] + lp[1]) + (lp[2] + lp[3]);
+    // out^T = V^T . P^T: the output column is the head (lane % 16), the lane
+    // that owns the head's running max, so the rescale above is per lane.
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+        f16x8 v0, v1;
+        int8x16_to_f16(vop[d], v0, v1);
+        st.acc[d] = mfma_16x16x32_f16(v0, pop[0], st.acc[d]);
+        st.acc[d] = mfma_16x16x32_f16(v1, pop[1], st.acc[d]);
+    }
+}
+
+// The q^T operand of query head `head` of sequence b (zeros for dead heads) and
+// its log2-domain score factor.
+template <int D>
+__device__ __forceinline__ float load_query(const DecodeArgs &a, int b, int head, bool head_ok,
+                                            int grp, i32x4 (&qop)[D / 64]) {
+    const int8_t *qrow = a.q + ((int64_t)b * a.q_heads + (head_ok ? head : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < D / 64; ++s)
+        qop[s] = head_ok ? *reinterpret_cast<const i32x4 *>(qrow + 64 * s + 16 * grp)
+                         : i32x4{0, 0, 0, 0};
+    float cq = 0.0f;
+    if (head_ok) {
+        cq = a.q_gran == REEF_SCALE_PER_TENSOR ? a.qs[0]
+             : a.q_gran == REEF_SCALE_PER_HEAD ? a.qs[head]
+                                                : a.qs[(int64_t)b * a.q_heads + head];
+    }
+    return cq * a.score_scale;
+}
+
+// Keys [k_begin, k_end) of (sequence b, kv head kvh) in steps of k_step, the next
+// block's loads (and the table entries of the one after) issued before the
+// current block is computed.
+template <int D, bool PAGED>
+__device__ __forceinline__ void run_keys(const DecodeArgs &a, int b, int kvh, int lo, int k_begin,
+                                         int k_end, int k_step, int n_pages,
+                                         const i32x4 (&qop)[D / 64], float c, int lane,
+                                         DecodeRun<D> &st, bool &bad_page) {
+    const int col = lane & 15, grp = lane >> 4;
+    DecodeBlock<D> cur, nxt;
+    if (k_begin < k_end)
+        load_block<D, PAGED>(a, b, kvh, k_begin, n_pages,
+                             fetch_pages<PAGED>(a, b, k_begin, n_pages, lane), col, grp, cur,
+                             bad_page);
+    int pg_next = fetch_pages<PAGED>(a, b, k_begin + k_step, n_pages, lane);
+    for (int kb = k_begin; kb < k_end; kb += k_step) {
+        const bool more = kb + k_step < k_end;
+        const int pg_after = fetch_pages<PAGED>(a, b, kb + 2 * k_step, n_pages, lane);
+        if (more) load_block<D, PAGED>(a, b, kvh, kb + k_step, n_pages, pg_next, col, grp, nxt, bad_page);
+        pg_next = pg_after;
+        block_math<D>(cur, kb, lo, k_end, qop, c, lane, st);
+        if (more) cur = nxt;
+    }
+}
+
+template <int D, bool PAGED>
+__global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs a, float *out) {
     constexpr int DB = D / 16;   // 16-wide output blocks
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -149,161 +369,25 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
     const int k_end = in_range ? len : 0;
     const int n_pages = (len + kPage - 1) / kPage;
 
-    // q^T operand: 16 bytes of head `head` per 64-wide reduction step.
-    i32x4 qop[KS];
-    const int8_t *qrow = a.q + ((int64_t)b * a.q_heads + (head_ok ? head : 0)) * D;
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-        qop[s] = head_ok ? *reinterpret_cast<const i32x4 *>(qrow + 64 * s + 16 * grp)
-                         : i32x4{0, 0, 0, 0};
-    float cq = 0.0f;
-    if (head_ok) {
-        cq = a.q_gran == REEF_SCALE_PER_TENSOR ? a.qs[0]
-             : a.q_gran == REEF_SCALE_PER_HEAD ? a.qs[head]
-                                                : a.qs[(int64_t)b * a.q_heads + head];
-    }
-    const float c = cq * a.score_scale;
-
-    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
+    i32x4 qop[D / 64];
+    const float c = load_query<D>(a, b, head, head_ok, grp, qop);
+    DecodeRun<D> st;
+    reset_run<D>(st);
+    bool bad_page = false;
+    run_keys<D, PAGED>(a, b, kvh, lo, k_begin, k_end, k_step, n_pages, qop, c, lane, st, bad_page);
+    float m_run = st.m_run, l_run = st.l_run, s_run = st.s_run;
     f32x4 acc[DB];
 #pragma unroll
-    for (int d = 0; d < DB; ++d) acc[d] = f32x4{};
-    bool bad_page = false;
-
-    // One 64-key block in registers: the operands of both matrix products and,
-    // per lane, the K and V scale of key 16 grp + col (the 16 lanes of a group
-    // hold the 16 scales of its page, handed around with shuffles). The next
-    // block's loads are issued before the current block is computed.
-    struct Block {
-        i32x4 k[4][KS];
-        i32x4 v[DB];
-        float ks, vs;
-        bool live;
-    };
-    auto load_block = [&](int kb, Block &x) {
-        const int page0 = kb / kPage;
-        // K rows for the score instruction: row m = col of block t is key
-        // 16 (m / 4) + 4t + (m % 4), in page m / 4.
-        const PageRef kp = page_ref<D, PAGED>(a, b, kvh, page0 + (col >> 2), n_pages);
-        // This lane group's page for scales, P and V.
-        const PageRef gp = page_ref<D, PAGED>(a, b, kvh, page0 + grp, n_pages);
-        bad_page |= !gp.ok;
-        x.live = gp.live;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-                x.k[t][s] = load_stream<!PAGED>(reinterpret_cast<const i32x4 *>(
-                    kp.k + (4 * t + (col & 3)) * D + 64 * s + 16 * grp));
-#pragma unroll
-        for (int d = 0; d < DB; ++d)
-            x.v[d] = load_stream<!PAGED>(
-                reinterpret_cast<const i32x4 *>(gp.vt + (16 * d + col) * kPage));
-        x.ks = gp.ks[col];
-        x.vs = gp.vs[col];
-    };
-    Block cur, nxt;
-    if (k_begin < k_end) load_block(k_begin, cur);
-    for (int kb = k_begin; kb < k_end; kb += k_step) {
-        const bool more = kb + k_step < k_end;
-        if (more) load_block(kb + k_step, nxt);
-        const auto &kop = cur.k;
-        const auto &vop = cur.v;
-        const int row0 = lane & ~15;  // first lane of this lane group
-        float ksc[16], vsc[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            ksc[r] = __shfl(cur.ks, row0 + r);
-            vsc[r] = __shfl(cur.vs, row0 + r);
-        }
-        const bool live_g = cur.live;
-
-        float x[16];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            i32x4 s = {0, 0, 0, 0};
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) s = mfma_16x16x64_i8(kop[t][ks], qop[ks], s);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[4 * t + i] = (float)s[i] * (c * ksc[4 * t + i]);
-        }
-        // Blocks wholly inside [lo, k_end) on live pages skip the masks. In the
-        // others, keys outside or on a dead page take no part: score -inf and
-        // value scale 0 (the cache past a sequence's end may hold anything).
-        const bool full = kb >= lo && kb + kBlockKeys <= k_end && __all(live_g);
-        float vv[16];
-        if (full) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) vv[r] = vsc[r];
-        } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kb + 16 * grp + r;
-                const bool vis = key >= lo && key < k_end && live_g;
-                if (!vis) x[r] = -INFINITY;
-                vv[r] = vis ? vsc[r] : 0.0f;
-            }
-        }
-        float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        float vmax = fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3]));
-#pragma unroll
-        for (int r = 4; r < 16; r += 2) {
-            mt = fmaxf(mt, fmaxf(x[r], x[r + 1]));
-            vmax = fmaxf(vmax, fmaxf(vv[r], vv[r + 1]));
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
-        vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
-
-        // Lazy rescale: the running max moves only when a head's block max exceeds
-        // it by more than 2^8, and the value normalizer s_run (values accumulate in
-        // units of s_run, the largest value scale so far) only when a value scale
-        // exceeds it 16-fold, so p * v_scale / s_run stays below 2^12 in fp16.
-        if (__any(mt > m_run + 8.0f || vmax > s_run * 16.0f)) {
-            const float m_new = fmaxf(m_run, mt);
-            const float s_new = fmaxf(s_run, vmax);
-            const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            const float alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
-            inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
-            m_run = m_new;
-            s_run = s_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
-        }
-        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-
-        // P operand: lane group g's keys 16g + 8h + e for the two halves h.
-        f16x8 pop[2];
-        float lp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p = __builtin_amdgcn_exp2f(x[r] - m_use);
-            lp[r & 3] += p;
-            pop[r >> 3][r & 7] = (_Float16)(p * (vv[r] * inv_s));
-        }
-        l_run += (lp[0] + lp[1]) + (lp[2] + lp[3]);
-        // out^T = V^T . P^T: the output column is the head (lane % 16), the lane
-        // that owns the head's running max, so the rescale above is per lane.
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-            f16x8 v0, v1;
-            int8x16_to_f16(vop[d], v0, v1);
-            acc[d] = mfma_16x16x32_f16(v0, pop[0], acc[d]);
-            acc[d] = mfma_16x16x32_f16(v1, pop[1], acc[d]);
-        }
-        if (more) cur = nxt;
-    }
+    for (int d = 0; d < DB; ++d) acc[d] = st.acc[d];
     if (bad_page) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
 
     // Row sums: this lane holds head col's partial over its 16 keys per block.
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
 
-    // The workgroup's 4 splits merge in LDS (log-sum-exp) into one partial, so the
-    // combine reads a quarter as many. Waves 1..3 hand over (max, sum, accumulator
-    // in value units) in a lane-linear layout; wave 0 merges and writes.
+    // The workgroup's 4 splits merge in LDS (log-sum-exp) into one part. Waves 1..3
+    // hand over (max, sum, accumulator in value units) in a lane-linear layout;
+    // wave 0 merges.
     __shared__ f32x4 sO[kDecodeWaves - 1][DB][kWave];
     __shared__ float2 sML[kDecodeWaves - 1][kWave];
     if (wave > 0) {
@@ -331,75 +415,105 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
         e[w] = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - m);
         l += lw[w] * e[w];
     }
-    // acc[d][i] is (channel 16 d + 4 grp + i, head col); write live heads.
-    const int64_t base_bh = (int64_t)b * a.q_heads + kvh * a.group;
-    const int g = blockIdx.x;  // this workgroup's partial
-    if (head_ok) {
-        float *po = a.part_o + ((base_bh + col) * a.groups + g) * D;
+    // acc[d][i] is (channel 16 d + 4 grp + i, head col): this part's output in
+    // absolute value units.
+    f32x4 o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+        o[d] = acc[d] * (s_run * e[0]);
+#pragma unroll
+        for (int w = 1; w < kDecodeWaves; ++w) o[d] += sO[w - 1][d][lane] * e[w];
+    }
+
+    // With more than one workgroup per (sequence, kv head), every part writes
+    // (max, sum, output) to its workspace slot with device-coherent stores, waits
+    // for them and counts itself in on the item's counter; the last part merges
+    // the slots in part order (its own from registers, explicit fused
+    // multiply-adds: the same result whichever part finishes last), stores the
+    // output and resets the counter. No second kernel combines splits.
+    const int parts = a.groups;
+    bool store = parts == 1;
+    if (parts > 1) {
+        const int item = b * a.kv_heads + kvh;
+        const int self = blockIdx.x;
+        uint64_t *slots = reinterpret_cast<uint64_t *>(a.slots) +
+                          (int64_t)item * parts * DecodeSlot<D>::ELEMS;
+        uint64_t *so = slots + (int64_t)self * DecodeSlot<D>::ELEMS;
+        auto pack = [](float x0, float x1) {
+            return (uint64_t)__float_as_uint(x0) | ((uint64_t)__float_as_uint(x1) << 32);
+        };
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
-            f32x4 o = acc[d] * (s_run * e[0]);
-#pragma unroll
-            for (int w = 1; w < kDecodeWaves; ++w) o += sO[w - 1][d][lane] * e[w];
-            *reinterpret_cast<f32x4 *>(po + 16 * d + 4 * grp) = o;
+            __hip_atomic_store(so + (2 * d) * kWave + lane, pack(o[d][0], o[d][1]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(so + (2 * d + 1) * kWave + lane, pack(o[d][2], o[d][3]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-    }
-    if (head_ok && grp == 0) {
-        float *ml = a.part_ml + ((base_bh + col) * a.groups + g) * 2;
-        ml[0] = m;
-        ml[1] = l;
-    }
-}
-
-// out[b, h, :] = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s, over
-// the splits that hold keys of sequence b (the others wrote nothing). One wave per
-// (b, h): lane s reads split s's (m, l); the output loop's loads are independent.
-template <int D>
-__global__ __launch_bounds__(64) void decode_combine(const float *__restrict__ part_o,
-                                                     const float *__restrict__ part_ml,
-                                                     DecodeArgs a, float *__restrict__ out) {
-    const int64_t bh = blockIdx.x;
-    const int lane = threadIdx.x;
-    const int splits = a.groups;
-    const int b = (int)(bh / a.q_heads);
-    int len = a.context_lens ? a.context_lens[b] : a.max_context;
-    if (len < 1 || len > a.max_context) len = 0;
-    const int lo = a.window > 0 ? max(0, len - a.window) : 0;
-    // split s is live when block lo / 64 + s starts before len; workgroup g (splits
-    // 4 g .. 4 g + 3) when its first split is
-    const int live_splits =
-        len > 0 ? min(a.splits, (len + kBlockKeys - 1) / kBlockKeys - lo / kBlockKeys) : 0;
-    const int live = (live_splits + kDecodeWaves - 1) / kDecodeWaves;
-    const float *ml = part_ml + bh * splits * 2;
-    const float *po = part_o + bh * splits * D;
-    float o[D / 64];
+        __hip_atomic_store(so + DecodeSlot<D>::O * kWave + lane, pack(m, l), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // the slot is complete before the count
+        uint32_t ticket = 0;
+        if (lane == 0)
+            ticket = __hip_atomic_fetch_add(a.counters + item, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+        ticket = __shfl(ticket, 0);
+        if (ticket != (uint32_t)(parts - 1)) return;
+        if (lane == 0)
+            __hip_atomic_store(a.counters + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        auto get = [](const uint64_t *q) {
+            return __hip_atomic_load(const_cast<uint64_t *>(q), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        };
+        auto lo32 = [](uint64_t v) { return __uint_as_float((uint32_t)v); };
+        auto hi32 = [](uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); };
+        float mt = m;
+        for (int p = 0; p < parts; ++p)
+            if (p != self)
+                mt = fmaxf(mt, lo32(get(slots + (int64_t)p * DecodeSlot<D>::ELEMS +
+                                        DecodeSlot<D>::O * kWave + lane)));
+        float lt = 0.0f;
+        f32x4 tot[DB];
 #pragma unroll
-    for (int j = 0; j < D / 64; ++j) o[j] = 0.0f;
-    float l = 0.0f;
-    // splits beyond 64 are folded in chunks of 64 lanes
-    float m = -INFINITY;
-    for (int s0 = 0; s0 < live; s0 += kWave) {
-        const int s = s0 + lane;
-        m = fmaxf(m, s < live ? ml[2 * s] : -INFINITY);
-    }
-    m = wave_max(m);
-    const float m_use = m == -INFINITY ? 0.0f : m;
-    for (int s0 = 0; s0 < live; s0 += kWave) {
-        const int s = s0 + lane;
-        const float w = s < live ? __builtin_amdgcn_exp2f(ml[2 * s] - m_use) : 0.0f;
-        l += s < live ? w * ml[2 * s + 1] : 0.0f;
-        const int n = min(kWave, live - s0);
-#pragma unroll 4
-        for (int i = 0; i < n; ++i) {
-            const float wi = __shfl(w, i);
+        for (int d = 0; d < DB; ++d) tot[d] = f32x4{};
+        for (int p = 0; p < parts; ++p) {
+            float mp, lp;
+            f32x4 op[DB];
+            if (p == self) {
+                mp = m;
+                lp = l;
 #pragma unroll
-            for (int j = 0; j < D / 64; ++j) o[j] += po[(int64_t)(s0 + i) * D + 64 * j + lane] * wi;
+                for (int d = 0; d < DB; ++d) op[d] = o[d];
+            } else {
+                const uint64_t *sl = slots + (int64_t)p * DecodeSlot<D>::ELEMS;
+                const uint64_t ml = get(sl + DecodeSlot<D>::O * kWave + lane);
+                mp = lo32(ml);
+                lp = hi32(ml);
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+                    const uint64_t v0 = get(sl + (2 * d) * kWave + lane);
+                    const uint64_t v1 = get(sl + (2 * d + 1) * kWave + lane);
+                    op[d] = f32x4{lo32(v0), hi32(v0), lo32(v1), hi32(v1)};
+                }
+            }
+            const float wp = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - mt);
+            lt = __builtin_fmaf(wp, lp, lt);
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) tot[d][i] = __builtin_fmaf(wp, op[d][i], tot[d][i]);
         }
-    }
-    l = wave_sum(l);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-    for (int j = 0; j < D / 64; ++j) out[bh * D + 64 * j + lane] = o[j] * inv;
+        for (int d = 0; d < DB; ++d) o[d] = tot[d];
+        l = lt;
+        store = true;
+    }
+    // A sequence with no keys (a bad length) ends with l = 0 and stores zeros.
+    if (store && head_ok) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float *orow = out + ((int64_t)b * a.q_heads + head) * D;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) *reinterpret_cast<f32x4 *>(orow + 16 * d + 4 * grp) = o[d] * inv;
+    }
 }
 
 __global__ void pack_v_pages(const int8_t *__restrict__ v_tokens, int64_t pages, int32_t dim,
@@ -446,12 +560,21 @@ reef_status validate(const reef_decode_params *p, const int8_t *q, const float *
     return REEF_OK;
 }
 
+// Workspace: one counter per (sequence, kv head), then, with more than one
+// workgroup (4 splits) per sequence, one part slot per workgroup.
+int64_t counter_bytes(const reef_decode_params *p) {
+    return ceil_div(p->batch * p->kv_heads * 4, 256) * 256;
+}
+
+int64_t workspace_bytes(const reef_decode_params *p) {
+    const int64_t groups = ceil_div(default_splits(p), kDecodeWaves);
+    const int64_t slot = (p->head_dim == 128 ? DecodeSlot<128>::ELEMS : DecodeSlot<64>::ELEMS) * 8;
+    return counter_bytes(p) + (groups > 1 ? p->batch * p->kv_heads * groups * slot : 0);
+}
+
 template <bool PAGED>
-reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out,
+reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out, void *workspace,
                           hipStream_t stream) {
-    const int splits = default_splits(p);
-    a.splits = splits;
-    a.groups = (int32_t)ceil_div(splits, kDecodeWaves);
     a.batch = (int32_t)p->batch;
     a.q_heads = (int32_t)p->q_heads;
     a.kv_heads = (int32_t)p->kv_heads;
@@ -460,26 +583,19 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
     a.window = (int32_t)std::min<int64_t>(p->window, INT32_MAX);
     a.q_gran = p->q_granularity;
     a.score_scale = p->softmax_scale * kLog2e;
-    const dim3 grid((unsigned)ceil_div(splits, kDecodeWaves), (unsigned)p->kv_heads,
-                    (unsigned)p->batch);
+    const int splits = default_splits(p);
+    a.splits = splits;
+    a.groups = (int32_t)ceil_div(splits, kDecodeWaves);
+    a.counters = static_cast<uint32_t *>(workspace);
+    a.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + counter_bytes(p));
+    const dim3 grid((unsigned)a.groups, (unsigned)p->kv_heads, (unsigned)p->batch);
     if (p->head_dim == 128)
-        hipLaunchKernelGGL((decode_kernel<128, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
-    else
-        hipLaunchKernelGGL((decode_kernel<64, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
-    const dim3 cgrid((unsigned)(p->batch * p->q_heads));
-    if (p->head_dim == 128)
-        hipLaunchKernelGGL(decode_combine<128>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml, a,
+        hipLaunchKernelGGL((decode_kernel<128, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a,
                            out);
     else
-        hipLaunchKernelGGL(decode_combine<64>, cgrid, dim3(64), 0, stream, a.part_o, a.part_ml, a,
+        hipLaunchKernelGGL((decode_kernel<64, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a,
                            out);
     return launch_status();
-}
-
-void set_workspace(DecodeArgs &a, const reef_decode_params *p, void *workspace) {
-    const int64_t rows = p->batch * p->q_heads * ceil_div(default_splits(p), kDecodeWaves);
-    a.part_o = static_cast<float *>(workspace);
-    a.part_ml = a.part_o + rows * p->head_dim;
 }
 
 }  // namespace
@@ -488,10 +604,10 @@ void set_workspace(DecodeArgs &a, const reef_decode_params *p, void *workspace) 
 using namespace reef;
 
 extern "C" size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p) {
-    if (!p || p->batch <= 0 || p->q_heads <= 0 || p->head_dim <= 0 || p->max_context <= 0)
+    if (!p || p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->head_dim <= 0 ||
+        p->max_context <= 0)
         return 0;
-    const int64_t rows = p->batch * p->q_heads * ceil_div(default_splits(p), kDecodeWaves);
-    return (size_t)(rows * (p->head_dim + 2) * sizeof(float));
+    return (size_t)workspace_bytes(p);
 }
 
 extern "C" reef_status reef_attention_decode_int8(const reef_decode_params *p, const int8_t *q,
@@ -515,8 +631,7 @@ extern "C" reef_status reef_attention_decode_int8(const reef_decode_params *p, c
     a.vs = v_scales;
     a.context_lens = context_lens;
     a.status = status_word;
-    set_workspace(a, p, workspace);
-    return launch_decode<false>(p, a, out, stream);
+    return launch_decode<false>(p, a, out, workspace, stream);
 }
 
 extern "C" reef_status reef_attention_decode_int8_paged(
@@ -545,8 +660,7 @@ extern "C" reef_status reef_attention_decode_int8_paged(
     a.status = status_word;
     a.max_blocks = (int32_t)max_blocks_per_seq;
     a.num_pages = (int32_t)num_pages;
-    set_workspace(a, p, workspace);
-    return launch_decode<true>(p, a, out, stream);
+    return launch_decode<true>(p, a, out, workspace, stream);
 }
 
 extern "C" reef_status reef_kv_pack_v_pages(const int8_t *v_tokens, int64_t pages,

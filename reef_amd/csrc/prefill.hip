@@ -830,15 +830,6 @@ bool valid_int8_strides(const reef_strides *s, const void *base) {
            s->head % 16 == 0 && s->token % 16 == 0;
 }
 
-// Compute units of the current device (one split workgroup fits on each).
-int64_t compute_units() {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
-    return n;
-}
-
 bool valid_granularity(int32_t g) {
     return g == REEF_SCALE_PER_TENSOR || g == REEF_SCALE_PER_HEAD || g == REEF_SCALE_PER_TOKEN;
 }

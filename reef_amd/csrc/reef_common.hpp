@@ -105,6 +105,15 @@ inline bool aligned(const void *p, size_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
+// Compute units of the current device (256 on MI355X; also the answer without one).
+inline int64_t compute_units() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
 inline reef_status launch_status() {
     return hipGetLastError() == hipSuccess ? REEF_OK : REEF_HIP_ERROR;
 }

@@ -91,7 +91,12 @@ def test_decode_host_validation_and_workspace():
     p = DecodeParams(batch=64, q_heads=32, kv_heads=8, head_dim=128, max_context=4096,
                      window=0, softmax_scale=0.1, q_granularity=2, num_splits=0, flags=0)
     ws = lib.reef_attention_decode_workspace_bytes(C.byref(p))
-    assert ws > 0 and ws % (64 * 32 * 130 * 4) == 0
+    # one counter per (sequence, kv head); 4 splits per sequence are one workgroup,
+    # so no part slots
+    assert ws == 2048
+    many = DecodeParams(64, 32, 8, 128, 4096, 0, 0.1, 2, 9, 0)
+    # 9 splits: 3 workgroups per sequence, each with a slot of 64 lanes x 17 eight-byte words
+    assert lib.reef_attention_decode_workspace_bytes(C.byref(many)) == 2048 + 64 * 8 * 3 * 17 * 64 * 8
     f = [_fake(i) for i in range(1, 12)]
     args = lambda pp, w: (C.byref(pp), f[0], f[1], f[2], f[3], f[4], f[5], None, f[6], f[7],  # noqa: E731
                           w, None, None)

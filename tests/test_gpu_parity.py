@@ -402,6 +402,44 @@ def test_decode_paged_matches_oracle(reef, B, Hq, Hkv, D, lens, window):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("paged,B,Hq,Hkv,D,window", [
+    (False, 300, 4, 2, 128, 0),   # 300 sequences x 2 kv heads
+    (True, 130, 8, 1, 128, 0),    # ragged pool, 8:1 grouping
+    (True, 40, 16, 2, 64, 300),   # window
+])
+def test_decode_ragged_merge_in_launch(reef, paged, B, Hq, Hkv, D, window):
+    """Sequences split over several workgroups are merged by the last of them in the
+    same launch: oracle tolerance, bit-identical on a second call (fixed merge
+    order), item counters back at zero, and another split count agrees."""
+    rng = np.random.default_rng(B + D)
+    lens = [int(x) for x in rng.integers(1, 1500, B)]
+    lens[0], lens[-1] = 1, 1500
+    max_ctx = ((max(lens) + 63) // 64) * 64
+    case(f"decode ragged paged={paged} B{B} Hq{Hq} Hkv{Hkv} D{D} win{window}")
+    qq, qs, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 61 + B, max_ctx)
+    scale = 1 / math.sqrt(D)
+    glens = gpu(np.array(lens, np.int32))
+    if paged:
+        kp, vp, ksp, vsp, table = _paged(kq, ks, vq, vs, lens, 63 + B)
+        args = (gpu(qq), gpu(qs), gpu(kp), gpu(vp), gpu(ksp), gpu(vsp), gpu(table), glens)
+        fn = reef.attention_decode_paged
+    else:
+        args = (gpu(qq), gpu(qs), gpu(kq), reef.pack_v_pages(gpu(vq)), gpu(ks), gpu(vs), glens)
+        fn = reef.attention_decode
+    p = reef._decode_params(gpu(qq), max_ctx, Hkv, window, scale, reef.PER_TOKEN, 0)
+    ws = reef.decode_workspace(p, "cuda")
+    out1 = host(fn(*args, window=window, softmax_scale=scale, workspace=ws))
+    out2 = host(fn(*args, window=window, softmax_scale=scale, workspace=ws))
+    fixed = host(fn(*args, window=window, softmax_scale=scale, num_splits=9))
+    gold = _decode_gold(qq, qs, kq, ks, vq, vs, lens, window, scale)
+    err = np.abs(out1 - gold).max()
+    print(f"max_abs_err {err:.3e} vs 9 splits {np.abs(out1 - fixed).max():.3e}", flush=True)
+    assert err <= TOL
+    assert np.abs(fixed - gold).max() <= TOL
+    assert np.array_equal(out1, out2)
+    assert not host(ws[:B * Hkv]).any()  # the counters lead the workspace
+
+
 def test_decode_paged_flags_bad_pages_and_lengths(reef):
     case("decode paged: out-of-range page and length are reported")
     B, Hq, Hkv, D, lens = 2, 4, 1, 64, [40, 30]
