@@ -187,6 +187,113 @@ __global__ __launch_bounds__(kQuantThreads) void head_quantize(HeadView v, const
     if (bad) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
 }
 
+// Flat form for heads whose tokens are contiguous (token stride == head_dim, both
+// multiples of 4): slice (b, h) is tokens * dim consecutive floats. Block (x, h, b)
+// streams float4 [x * chunk, (x + 1) * chunk) of its slice, kFlatUnroll independent
+// loads in flight per thread, no per-row index arithmetic. Three launches and no
+// atomics: every block's largest magnitude goes to a partial word (kept in the
+// output buffer q, which the quantize pass overwrites afterwards), one block per
+// head reduces its partials and writes the head's scale, and the quantize pass
+// reads that scale. (Atomic maxima into the scales array serialize: the heads'
+// words share one cache line.)
+struct FlatHeads {
+    const float *x;
+    int64_t sb, sh;      // element strides of batch and head
+    int64_t slice4;      // float4 per (batch, head) slice
+    int64_t chunk4;      // float4 per block
+    int32_t heads, batch, blocks;  // blocks per slice
+};
+
+constexpr int kFlatUnroll = 8;
+
+__device__ __forceinline__ uint32_t block_max(uint32_t m) {  // the result on thread 0
+    __shared__ uint32_t partial[kQuantThreads / kWave];
+    m = wave_max_u32(m);
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    if (lane == 0) partial[wave] = m;
+    __syncthreads();
+    uint32_t r = partial[0];
+    for (int w = 1; w < kQuantThreads / kWave; ++w) r = r > partial[w] ? r : partial[w];
+    return r;
+}
+
+__global__ __launch_bounds__(kQuantThreads) void head_max_flat(FlatHeads f, uint32_t *partials) {
+    const int h = blockIdx.y, b = blockIdx.z;
+    const float4 *x = reinterpret_cast<const float4 *>(f.x + b * f.sb + h * f.sh);
+    const int64_t i0 = (int64_t)blockIdx.x * f.chunk4;
+    const int64_t i1 = min(f.slice4, i0 + f.chunk4);
+    uint32_t m = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += kQuantThreads * kFlatUnroll) {
+        float4 v[kFlatUnroll];
+#pragma unroll
+        for (int u = 0; u < kFlatUnroll; ++u) {
+            const int64_t j = i + u * kQuantThreads;
+            v[u] = j < i1 ? x[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < kFlatUnroll; ++u) {
+            uint32_t a = mag_bits(v[u].x), c = mag_bits(v[u].y), d = mag_bits(v[u].z),
+                     e = mag_bits(v[u].w);
+            a = a > c ? a : c;
+            d = d > e ? d : e;
+            a = a > d ? a : d;
+            m = m > a ? m : a;
+        }
+    }
+    m = block_max(m);
+    if (threadIdx.x == 0) partials[((int64_t)h * f.batch + b) * f.blocks + blockIdx.x] = m;
+}
+
+// One block per head: the largest of its partials, then the head's scale.
+__global__ __launch_bounds__(kQuantThreads) void head_scale_flat(FlatHeads f,
+                                                                 const uint32_t *partials,
+                                                                 float *scales) {
+    const int h = blockIdx.x;
+    const int n = f.batch * f.blocks;
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < n; i += kQuantThreads) {
+        const uint32_t a = partials[(int64_t)h * n + i];
+        m = m > a ? m : a;
+    }
+    m = block_max(m);
+    if (threadIdx.x == 0) scales[h] = int8_scale(__uint_as_float(m));
+}
+
+__global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f,
+                                                                    const float *scales,
+                                                                    int8_t *__restrict__ q,
+                                                                    uint32_t *status) {
+    const int h = blockIdx.y, b = blockIdx.z;
+    const float scale = scales[h];
+    const float4 *x = reinterpret_cast<const float4 *>(f.x + b * f.sb + h * f.sh);
+    char4 *out = reinterpret_cast<char4 *>(q) + ((int64_t)b * f.heads + h) * f.slice4;
+    const int64_t i0 = (int64_t)blockIdx.x * f.chunk4;
+    const int64_t i1 = min(f.slice4, i0 + f.chunk4);
+    bool bad = false;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += kQuantThreads * kFlatUnroll) {
+        float4 v[kFlatUnroll];
+#pragma unroll
+        for (int u = 0; u < kFlatUnroll; ++u) {
+            const int64_t j = i + u * kQuantThreads;
+            v[u] = j < i1 ? x[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < kFlatUnroll; ++u) {
+            const int64_t j = i + u * kQuantThreads;
+            if (j >= i1) break;
+            bad |= !(__builtin_isfinite(v[u].x) && __builtin_isfinite(v[u].y) &&
+                     __builtin_isfinite(v[u].z) && __builtin_isfinite(v[u].w));
+            char4 c;
+            c.x = quantize_int8(v[u].x, scale);
+            c.y = quantize_int8(v[u].y, scale);
+            c.z = quantize_int8(v[u].z, scale);
+            c.w = quantize_int8(v[u].w, scale);
+            out[j] = c;
+        }
+    }
+    if (bad) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
+}
+
 // ---- per token (quantize_rows) --------------------------------------------------------------
 //
 // Fast form for rows of at most 256 float4 (width % 4 == 0): LPR lanes per row hold
@@ -393,6 +500,33 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
     v.per_row = (int32_t)(vec ? head_dim / 4 : head_dim);
     v.tpr = 1;
     while (v.tpr < v.per_row && v.tpr < kQuantThreads) v.tpr *= 2;
+    if (vec && v.st == head_dim && batch <= 65535) {
+        // Contiguous tokens: flat float4 streams, about 512 blocks in all (2 per
+        // compute unit), at least 32 KB of input each; the partial maxima (4 bytes
+        // per block) fit in q when q holds at least that many bytes.
+        FlatHeads f;
+        f.x = x;
+        f.sb = v.sb;
+        f.sh = v.sh;
+        f.slice4 = tokens * head_dim / 4;
+        f.heads = (int32_t)heads;
+        f.batch = (int32_t)batch;
+        const int64_t per_slice = std::max<int64_t>(
+            1, std::min(ceil_div(512, batch * heads), ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
+        f.chunk4 = ceil_div(f.slice4, per_slice);
+        f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
+        const int64_t partial_bytes = 4 * batch * heads * (int64_t)f.blocks;
+        if (partial_bytes <= batch * heads * tokens * head_dim && aligned(q, 4)) {
+            uint32_t *partials = reinterpret_cast<uint32_t *>(q);
+            const dim3 fgrid((unsigned)f.blocks, (unsigned)heads, (unsigned)batch);
+            hipLaunchKernelGGL(head_max_flat, fgrid, dim3(kQuantThreads), 0, stream, f, partials);
+            hipLaunchKernelGGL(head_scale_flat, dim3((unsigned)heads), dim3(kQuantThreads), 0, stream,
+                               f, (const uint32_t *)partials, scales);
+            hipLaunchKernelGGL(head_quantize_flat, fgrid, dim3(kQuantThreads), 0, stream, f,
+                               (const float *)scales, q, status_word);
+            return launch_status();
+        }
+    }
     uint32_t *bits = reinterpret_cast<uint32_t *>(scales);
     hipLaunchKernelGGL(zero_words, dim3((unsigned)ceil_div(heads, 64)), dim3(64), 0, stream, bits,
                        heads);

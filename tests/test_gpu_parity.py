@@ -105,6 +105,21 @@ def test_quantize_per_head_bit_exact_with_strides(reef):
     assert host(s)[5] == 1.0
 
 
+@pytest.mark.parametrize("B,H,S,D", [(3, 5, 77, 128), (1, 32, 2048, 128), (2, 3, 5, 64),
+                                     (1, 2, 1, 4)])
+def test_quantize_per_head_contiguous_bit_exact(reef, B, H, S, D):
+    """Contiguous heads take the flat streaming kernels: partial chunks, a zero head
+    and a large head, bit-exact against the oracle."""
+    case(f"quantize_per_head contiguous [{B}, {H}, {S}, {D}]")
+    x = W.lcg_normal(23 + S, B * H * S * D).reshape(B, H, S, D)
+    x[:, 0] *= 50.0
+    x[:, H - 1] = 0.0 if H > 1 else x[:, H - 1]
+    q, s = reef.quantize_per_head(gpu(x))
+    qo, so = oracle.quantize_per_head(x)
+    assert np.array_equal(host(s).view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(host(q), qo)
+
+
 @pytest.mark.parametrize("rows,width", [(4096, 128), (7, 37), (300, 64), (3, 1), (33, 96),
                                         (40, 2048), (9, 5000), (17, 8192), (5, 8193)])
 def test_quantize_rows_bit_exact(reef, rows, width):
