@@ -466,6 +466,28 @@ extern "C" reef_status reef_quantize_int8_per_tensor(const float *x, int64_t n, 
                                                      hipStream_t stream) {
     if (n <= 0 || !x || !q || !scale || !aligned(x, 16) || !aligned(q, 4))
         return REEF_INVALID_ARGUMENT;
+    if (n % 4 == 0) {
+        // One flat slice: the per-head kernels with a single head.
+        FlatHeads f;
+        f.x = x;
+        f.sb = f.sh = 0;
+        f.slice4 = n / 4;
+        f.heads = f.batch = 1;
+        const int64_t per_slice =
+            std::max<int64_t>(1, std::min<int64_t>(512, ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
+        f.chunk4 = ceil_div(f.slice4, per_slice);
+        f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
+        if (4 * (int64_t)f.blocks <= n) {
+            uint32_t *partials = reinterpret_cast<uint32_t *>(q);
+            hipLaunchKernelGGL(head_max_flat, dim3((unsigned)f.blocks), dim3(kQuantThreads), 0, stream,
+                               f, partials);
+            hipLaunchKernelGGL(head_scale_flat, dim3(1), dim3(kQuantThreads), 0, stream, f,
+                               (const uint32_t *)partials, scale);
+            hipLaunchKernelGGL(head_quantize_flat, dim3((unsigned)f.blocks), dim3(kQuantThreads), 0,
+                               stream, f, (const float *)scale, q, status_word);
+            return launch_status();
+        }
+    }
     uint32_t *bits = reinterpret_cast<uint32_t *>(scale);
     hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, stream, bits, (int64_t)1);
     const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(n / 4 + 1, kQuantThreads * 8)));

@@ -76,6 +76,22 @@ def _ties(n):
     return x
 
 
+@pytest.mark.parametrize("n", [4, 64, 4096 * 257, 33_554_432])
+def test_quantize_per_tensor_flat_bit_exact(reef, n):
+    """Sizes that are multiples of 4 take the flat streaming kernels (block maxima
+    in the output buffer, one reduction, quantize)."""
+    case(f"quantize_per_tensor flat n={n}")
+    x = (W.lcg_normal(24 + n % 97, n) * 2.5).astype(np.float32)
+    x[n // 3] = -40.0
+    q, s = reef.quantize_per_tensor(gpu(x))
+    qo, so = oracle.quantize_per_tensor(x)
+    assert host(s)[0].view(np.uint32) == so[0].view(np.uint32)
+    assert np.array_equal(host(q), qo)
+    z = np.zeros(n, np.float32)
+    q, s = reef.quantize_per_tensor(gpu(z))
+    assert host(s)[0] == 1.0 and not host(q).any()
+
+
 def test_quantize_per_tensor_bit_exact(reef):
     case("quantize_per_tensor n=1000003 normal + ties")
     x = (W.lcg_normal(21, 1_000_003) * 3.7).astype(np.float32)
