@@ -223,7 +223,7 @@ PREFILL_CASES = [
     (2, 2, 2, 77, 77, 128, None, 0, 2, 1, 1.0),          # engine's unscaled scores
     (1, 1, 1, 1, 1, 64, None, 0, 1, 1, None),            # a single token
     (1, 4, 4, 513, 513, 128, None, 0, 1, 2, None),       # per-token K/V scales
-    # log2-domain score scales near and past the limit of the biased score reads
+    # very large log2-domain score scales: rows dominated by one key (peaked softmax)
     (1, 2, 2, 256, 256, 128, None, 0, 1, 1, 3000.0),
     (1, 2, 1, 200, 300, 64, None, 0, 0, 0, 20000.0),
 ]
