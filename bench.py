@@ -166,7 +166,7 @@ def quant_graph_ms(torch, launch, steps=20, warmup=3):
     except Exception as e:  # noqa: BLE001
         print(f"# quantize graph timing unavailable ({e}); timing eager launches", file=sys.stderr)
         return timed(torch, launch, steps, warmup)[1], "eager launches"
-    return timed(torch, g.replay, steps, warmup)[1], "one HIP graph of the 9 launches"
+    return timed(torch, g.replay, steps, warmup)[1], "one HIP graph of the launches"
 
 
 def bench_prefill(torch, reef, W, args):
@@ -475,7 +475,7 @@ def main():
                      "kernel": "prefill_kernel<128, false, false>",
                      "kernel_ms": round(kern_ms, 5), "algorithmic_ops_per_launch": ops},
         "quantize": {"kernels": "per-head quantize of q, k and v (per tensor: block maxima, "
-                                "head scales, quantize)",
+                                "then scales and quantize)",
                      "timing": quant_how,
                      "ms": round(quant_ms, 4),
                      "GB/s": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1)},

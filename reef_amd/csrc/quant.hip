@@ -190,12 +190,16 @@ __global__ __launch_bounds__(kQuantThreads) void head_quantize(HeadView v, const
 // Flat form for heads whose tokens are contiguous (token stride == head_dim, both
 // multiples of 4): slice (b, h) is tokens * dim consecutive floats. Block (x, h, b)
 // streams float4 [x * chunk, (x + 1) * chunk) of its slice, kFlatUnroll independent
-// loads in flight per thread, no per-row index arithmetic. Three launches and no
-// atomics: every block's largest magnitude goes to a partial word (kept in the
-// output buffer q, which the quantize pass overwrites afterwards), one block per
-// head reduces its partials and writes the head's scale, and the quantize pass
-// reads that scale. (Atomic maxima into the scales array serialize: the heads'
-// words share one cache line.)
+// loads in flight per thread, no per-row index arithmetic. No atomics (atomic maxima
+// into the scales array serialize: the heads' words share one cache line); every
+// block's largest magnitude goes to partial words kept in the output buffer q,
+// which the quantize pass overwrites afterwards. Two launches when every chunk of
+// q holds the batch * blocks partials of its head ("spread"): the max pass writes
+// its word into the chunk of every block of the same head, and each quantize block
+// reduces the words in its own chunk (the same maximum, so the same scale, in every
+// block of a head) before it overwrites that chunk, which no other block reads.
+// Otherwise three: the partials go to the front of q, one block per head reduces
+// them and writes the scale, and the quantize pass reads the scales.
 struct FlatHeads {
     const float *x;
     int64_t sb, sh;      // element strides of batch and head
@@ -217,6 +221,12 @@ __device__ __forceinline__ uint32_t block_max(uint32_t m) {  // the result on th
     return r;
 }
 
+// Word offset in q of the chunk of block (x, h, b).
+__device__ __forceinline__ int64_t chunk_word(const FlatHeads &f, int b, int h, int x) {
+    return ((int64_t)b * f.heads + h) * f.slice4 + (int64_t)x * f.chunk4;
+}
+
+template <bool kSpread>
 __global__ __launch_bounds__(kQuantThreads) void head_max_flat(FlatHeads f, uint32_t *partials) {
     const int h = blockIdx.y, b = blockIdx.z;
     const float4 *x = reinterpret_cast<const float4 *>(f.x + b * f.sb + h * f.sh);
@@ -241,7 +251,14 @@ __global__ __launch_bounds__(kQuantThreads) void head_max_flat(FlatHeads f, uint
         }
     }
     m = block_max(m);
-    if (threadIdx.x == 0) partials[((int64_t)h * f.batch + b) * f.blocks + blockIdx.x] = m;
+    if (kSpread) {
+        // partials is q: word b * blocks + x of the chunk of every block of head h
+        const int n = f.batch * f.blocks;
+        for (int i = threadIdx.x; i < n; i += kQuantThreads)
+            partials[chunk_word(f, i / f.blocks, h, i % f.blocks) + b * f.blocks + blockIdx.x] = m;
+    } else if (threadIdx.x == 0) {
+        partials[((int64_t)h * f.batch + b) * f.blocks + blockIdx.x] = m;
+    }
 }
 
 // One block per head: the largest of its partials, then the head's scale.
@@ -259,12 +276,29 @@ __global__ __launch_bounds__(kQuantThreads) void head_scale_flat(FlatHeads f,
     if (threadIdx.x == 0) scales[h] = int8_scale(__uint_as_float(m));
 }
 
-__global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f,
-                                                                    const float *scales,
+// kSpread: the scale comes from the partial words in this block's own chunk of q
+// (written by the max pass), and block (0, h, 0) stores it to scales[h].
+template <bool kSpread>
+__global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f, float *scales,
                                                                     int8_t *__restrict__ q,
                                                                     uint32_t *status) {
     const int h = blockIdx.y, b = blockIdx.z;
-    const float scale = scales[h];
+    float scale;
+    if (kSpread) {
+        const uint32_t *words = reinterpret_cast<const uint32_t *>(q) + chunk_word(f, b, h, blockIdx.x);
+        uint32_t m = 0;
+        for (int i = threadIdx.x; i < f.batch * f.blocks; i += kQuantThreads) {
+            const uint32_t a = words[i];
+            m = m > a ? m : a;
+        }
+        // every thread's reads are consumed before block_max's barrier, so the
+        // chunk may be overwritten after it
+        m = block_max(m);
+        scale = int8_scale(__uint_as_float(m));
+        if (b == 0 && blockIdx.x == 0 && threadIdx.x == 0) scales[h] = scale;
+    } else {
+        scale = scales[h];
+    }
     const float4 *x = reinterpret_cast<const float4 *>(f.x + b * f.sb + h * f.sh);
     char4 *out = reinterpret_cast<char4 *>(q) + ((int64_t)b * f.heads + h) * f.slice4;
     const int64_t i0 = (int64_t)blockIdx.x * f.chunk4;
@@ -456,6 +490,27 @@ int grid_for(int64_t work_items, int64_t cap = 4096) {
     return (int)(g < cap ? g : cap);
 }
 
+// The flat kernels over f (q 4-byte aligned, at least 4 * batch * heads * blocks
+// bytes): two launches when the shortest chunk of q holds a head's batch * blocks
+// partial words, three otherwise.
+void launch_flat(const FlatHeads &f, int8_t *q, float *scales, uint32_t *status,
+                 hipStream_t stream) {
+    uint32_t *partials = reinterpret_cast<uint32_t *>(q);
+    const dim3 grid((unsigned)f.blocks, (unsigned)f.heads, (unsigned)f.batch);
+    const int64_t last4 = f.slice4 - (int64_t)(f.blocks - 1) * f.chunk4;  // shortest chunk
+    if ((int64_t)f.batch * f.blocks <= std::min<int64_t>(last4, 512)) {
+        hipLaunchKernelGGL(head_max_flat<true>, grid, dim3(kQuantThreads), 0, stream, f, partials);
+        hipLaunchKernelGGL(head_quantize_flat<true>, grid, dim3(kQuantThreads), 0, stream, f,
+                           scales, q, status);
+        return;
+    }
+    hipLaunchKernelGGL(head_max_flat<false>, grid, dim3(kQuantThreads), 0, stream, f, partials);
+    hipLaunchKernelGGL(head_scale_flat, dim3((unsigned)f.heads), dim3(kQuantThreads), 0, stream,
+                       f, (const uint32_t *)partials, scales);
+    hipLaunchKernelGGL(head_quantize_flat<false>, grid, dim3(kQuantThreads), 0, stream, f,
+                       scales, q, status);
+}
+
 }  // namespace
 }  // namespace reef
 
@@ -478,13 +533,7 @@ extern "C" reef_status reef_quantize_int8_per_tensor(const float *x, int64_t n, 
         f.chunk4 = ceil_div(f.slice4, per_slice);
         f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
         if (4 * (int64_t)f.blocks <= n) {
-            uint32_t *partials = reinterpret_cast<uint32_t *>(q);
-            hipLaunchKernelGGL(head_max_flat, dim3((unsigned)f.blocks), dim3(kQuantThreads), 0, stream,
-                               f, partials);
-            hipLaunchKernelGGL(head_scale_flat, dim3(1), dim3(kQuantThreads), 0, stream, f,
-                               (const uint32_t *)partials, scale);
-            hipLaunchKernelGGL(head_quantize_flat, dim3((unsigned)f.blocks), dim3(kQuantThreads), 0,
-                               stream, f, (const float *)scale, q, status_word);
+            launch_flat(f, q, scale, status_word, stream);
             return launch_status();
         }
     }
@@ -539,13 +588,7 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
         f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
         const int64_t partial_bytes = 4 * batch * heads * (int64_t)f.blocks;
         if (partial_bytes <= batch * heads * tokens * head_dim && aligned(q, 4)) {
-            uint32_t *partials = reinterpret_cast<uint32_t *>(q);
-            const dim3 fgrid((unsigned)f.blocks, (unsigned)heads, (unsigned)batch);
-            hipLaunchKernelGGL(head_max_flat, fgrid, dim3(kQuantThreads), 0, stream, f, partials);
-            hipLaunchKernelGGL(head_scale_flat, dim3((unsigned)heads), dim3(kQuantThreads), 0, stream,
-                               f, (const uint32_t *)partials, scales);
-            hipLaunchKernelGGL(head_quantize_flat, fgrid, dim3(kQuantThreads), 0, stream, f,
-                               (const float *)scales, q, status_word);
+            launch_flat(f, q, scales, status_word, stream);
             return launch_status();
         }
     }

@@ -122,10 +122,12 @@ def test_quantize_per_head_bit_exact_with_strides(reef):
 
 
 @pytest.mark.parametrize("B,H,S,D", [(3, 5, 77, 128), (1, 32, 2048, 128), (2, 3, 5, 64),
-                                     (1, 2, 1, 4)])
+                                     (1, 2, 1, 4), (600, 2, 2, 8), (3, 5, 1, 8)])
 def test_quantize_per_head_contiguous_bit_exact(reef, B, H, S, D):
     """Contiguous heads take the flat streaming kernels: partial chunks, a zero head
-    and a large head, bit-exact against the oracle."""
+    and a large head, bit-exact against the oracle. The last two shapes have output
+    chunks shorter than a head's partial count (600 batches; 2-word chunks for 3
+    partials), so their maxima are reduced by the separate scale pass."""
     case(f"quantize_per_head contiguous [{B}, {H}, {S}, {D}]")
     x = W.lcg_normal(23 + S, B * H * S * D).reshape(B, H, S, D)
     x[:, 0] *= 50.0
