@@ -9,7 +9,10 @@
 // The weights depend on the row's final maximum and the probabilities on the
 // final sum, so the keys are visited three times (maximum, sum, output), each
 // time recomputing the exact int32 scores on v_mfma_i32_32x32x32_i8 rather than
-// storing them. p * v runs on v_mfma_f32_32x32x16_f16: p <= 255 and v are exact
+// storing them (the next tile's K operands load while a tile is processed; tiles
+// that every row of a wave sees skip the per-key mask). p * v runs on
+// v_mfma_f32_32x32x16_f16 with the value tile staged once per workgroup as fp16
+// in channel-major rows (one 16-byte LDS read per operand): p <= 255 and v are exact
 // in fp16, and every partial sum is an integer below 2^24 (at most 510 keys can
 // carry p > 0 beyond the ~255 the probabilities sum to, so |sum| <= 128 * 510),
 // so the fp32 accumulation is exact and the result is the engine's integer.
@@ -39,31 +42,67 @@ __device__ __forceinline__ int int_key_of_row(int m) {
     return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
 }
 
-// Scores of a 32-key block for this lane's query: register r of lane group g is
-// key kb + 16 g + r. Keys past kv_len read key 0 (their scores are masked).
+// K operands of one 64-key tile for this lane: block u (keys kt + 32 u ...), step
+// t of the head dimension. Row m of a block is key int_key_of_row(m); keys past
+// kv_len read key 0 (their scores are masked).
 template <int D>
-__device__ __forceinline__ i32x16 int_scores(const i32x4 (&qop)[D / 32], const int8_t *kbase,
-                                             int64_t k_st, int kb, int kv_len, int col, int grp) {
-    const int key = kb + int_key_of_row(col);
-    const int8_t *krow = kbase + (int64_t)(key < kv_len ? key : 0) * k_st;
+struct KTile {
+    i32x4 op[2][D / 32];
+};
+
+template <int D>
+__device__ __forceinline__ void load_k_tile(KTile<D> &k, const int8_t *kbase, int64_t k_st,
+                                            int kt, int kv_len, int col, int grp) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int key = kt + 32 * u + int_key_of_row(col);
+        const int8_t *krow = kbase + (int64_t)(key < kv_len ? key : 0) * k_st;
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+            k.op[u][t] = *reinterpret_cast<const i32x4 *>(krow + 32 * t + 16 * grp);
+    }
+}
+
+// Scores of 32-key block u for this lane's query: register r of lane group g is
+// key kt + 32 u + 16 g + r.
+template <int D>
+__device__ __forceinline__ i32x16 tile_scores(const KTile<D> &k, int u, const i32x4 (&qop)[D / 32]) {
     i32x16 s = {};
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t) {
-        const i32x4 kop = *reinterpret_cast<const i32x4 *>(krow + 32 * t + 16 * grp);
-        s = mfma_32x32x32_i8(kop, qop[t], s);
-    }
+    for (int t = 0; t < D / 32; ++t) s = mfma_32x32x32_i8(k.op[u][t], qop[t], s);
     return s;
+}
+
+// f(kt, k) for the tiles kt = t0, t0 + 64, ..., t1 with their K operands, the next
+// tile's loads in flight while f runs (two buffers taken in turn, no copies).
+template <int D, typename F>
+__device__ __forceinline__ void for_k_tiles(int t0, int t1, const int8_t *kbase, int64_t k_st,
+                                            int kv_len, int col, int grp, F f) {
+    KTile<D> ka, kb;
+    if (t0 <= t1) load_k_tile<D>(ka, kbase, k_st, t0, kv_len, col, grp);
+    for (int kt = t0; kt <= t1; kt += 2 * kIntKeys) {
+        if (kt + kIntKeys <= t1) load_k_tile<D>(kb, kbase, k_st, kt + kIntKeys, kv_len, col, grp);
+        f(kt, ka);
+        if (kt + kIntKeys > t1) break;
+        if (kt + 2 * kIntKeys <= t1) load_k_tile<D>(ka, kbase, k_st, kt + 2 * kIntKeys, kv_len, col, grp);
+        f(kt + kIntKeys, kb);
+    }
 }
 
 __device__ __forceinline__ int32_t rounding_shift_dev(int32_t value, int shift) {
     return shift == 0 ? value : (value >> shift) + ((value >> (shift - 1)) & 1);
 }
 
+// The value tile in LDS: fp16, channel-major (row c holds the tile's 64 keys of
+// channel c), rows padded to 72 halves so that the 16-byte operand reads of 8
+// consecutive channels fall in distinct banks.
+constexpr int kVRow = kIntKeys + 8;
+
 template <int D>
-__global__ __launch_bounds__(kIntThreads) void int_head_kernel(IntHeadArgs a) {
+__global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a) {
     constexpr int DB = D / 32;
     __shared__ uint16_t sTable[256];
-    __shared__ __attribute__((aligned(16))) int8_t sV[kIntKeys * D];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[D * kVRow];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -95,30 +134,45 @@ __global__ __launch_bounds__(kIntThreads) void int_head_kernel(IntHeadArgs a) {
     const bool wave_active = w_first < a.q_len;
     const int wk_lo = a.window > 0 ? max(0, a.query_start + w_first + 1 - a.window) : 0;
     const int wk_hi = min(a.query_start + w_last, a.kv_len - 1);
+    // Keys every valid row of the wave sees: [full_lo, full_hi].
+    const int full_lo = a.window > 0 ? max(0, a.query_start + w_last + 1 - a.window) : 0;
+    const int full_hi = min(a.query_start + w_first, a.kv_len - 1);
     const int r_last = min(q0 + kIntRows, a.q_len) - 1;
     const int key_lo = a.window > 0 ? max(0, a.query_start + q0 + 1 - a.window) : 0;
     const int key_hi = min(a.query_start + r_last, a.kv_len - 1);
     const int kt0 = key_lo / kIntKeys * kIntKeys;
+    // The wave's tiles: [wt0, wt1] (empty when the wave holds no row).
+    const int wt0 = wk_lo / kIntKeys * kIntKeys;
+    const int wt1 = wave_active ? wk_hi / kIntKeys * kIntKeys : wt0 - kIntKeys;
 
     const int8_t *kbase = a.k + b * a.k_sb + kvh * a.k_sh;
     const int8_t *vbase = a.v + b * a.v_sb + kvh * a.v_sh;
     __syncthreads();  // the table
 
-    auto visible = [&](int key) { return key >= lo && key <= hi; };
-    auto wave_needs = [&](int kt) { return wave_active && kt <= wk_hi && kt + kIntKeys - 1 >= wk_lo; };
+    // lo <= key <= hi as one unsigned compare (a select, not a branch)
+    auto visible = [&](int key) { return (uint32_t)(key - lo) <= (uint32_t)(hi - lo); };
+    // Every valid row of the wave sees every key of tile kt: no per-key mask.
+    auto tile_full = [&](int kt) { return kt >= full_lo && kt + kIntKeys - 1 <= full_hi; };
 
+    // The per-key work below is branch-free: a tile is either seen whole by every
+    // row of the wave (wave-uniform test, no mask) or masked with selects.
     // Pass 1: the row maximum over visible keys (int8.hpp:197-203).
     int32_t mx = INT32_MIN;
-    for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
-        if (!wave_needs(kt)) continue;
+    for_k_tiles<D>(wt0, wt1, kbase, a.k_st, a.kv_len, col, grp, [&](int kt, const KTile<D> &k) {
+        const i32x16 s[2] = {tile_scores<D>(k, 0, qop), tile_scores<D>(k, 1, qop)};
+        if (tile_full(kt)) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const i32x16 s = int_scores<D>(qop, kbase, a.k_st, kt + 32 * u, a.kv_len, col, grp);
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (visible(kt + 32 * u + 16 * grp + r)) mx = max(mx, s[r]);
+                for (int r = 0; r < 16; ++r) mx = max(mx, s[u][r]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    mx = max(mx, visible(kt + 32 * u + 16 * grp + r) ? s[u][r] : INT32_MIN);
         }
-    }
+    });
     {
         const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)mx, (uint32_t)mx, false, false);
         mx = max((int32_t)sw[0], (int32_t)sw[1]);
@@ -126,20 +180,27 @@ __global__ __launch_bounds__(kIntThreads) void int_head_kernel(IntHeadArgs a) {
 
     // Pass 2: the sum of table weights (:208-217).
     uint32_t sum = 0;
-    for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
-        if (!wave_needs(kt)) continue;
+    auto weight = [&](int32_t sc) {
+        const uint32_t d = (uint32_t)((mx - sc) >> a.score_shift);
+        return (uint32_t)sTable[d < 255u ? d : 255u];
+    };
+    for_k_tiles<D>(wt0, wt1, kbase, a.k_st, a.kv_len, col, grp, [&](int kt, const KTile<D> &k) {
+        const i32x16 s[2] = {tile_scores<D>(k, 0, qop), tile_scores<D>(k, 1, qop)};
+        if (tile_full(kt)) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const i32x16 s = int_scores<D>(qop, kbase, a.k_st, kt + 32 * u, a.kv_len, col, grp);
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if (visible(kt + 32 * u + 16 * grp + r)) {
-                    const uint32_t d = (uint32_t)((mx - s[r]) >> a.score_shift);
-                    sum += sTable[d < 255u ? d : 255u];
+                for (int r = 0; r < 16; ++r) sum += weight(s[u][r]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t w = weight(s[u][r]);  // any d indexes the table
+                    sum += visible(kt + 32 * u + 16 * grp + r) ? w : 0u;
                 }
-            }
         }
-    }
+    });
     {
         const auto sw = __builtin_amdgcn_permlane32_swap(sum, sum, false, false);
         sum = sw[0] + sw[1];
@@ -148,38 +209,61 @@ __global__ __launch_bounds__(kIntThreads) void int_head_kernel(IntHeadArgs a) {
     // sees a key; rows outside the tensor never store.
     const uint32_t recip = sum > 0 ? (255u << 16) / sum : 0u;
 
-    // Pass 3: probabilities and P.V (:218-227, 268-276). The value tile is staged
-    // token-major in LDS; each lane gathers its 8 keys of one channel.
+    // Pass 3: probabilities and P.V (:218-227, 268-276). Thread i < 2 D stages
+    // keys 2 (i % 32) and 2 (i % 32) + 1, channels 16 (i / 32) .. + 15 of each
+    // value tile: 16-byte loads one tile ahead, converted exactly to fp16 and
+    // stored as key pairs into the channel-major LDS tile. Each lane then reads
+    // its 8 keys of one channel as one 16-byte operand.
+    const bool stager = tid < 2 * D;
+    const int vkp = tid % 32, vc16 = tid / 32;
+    i32x4 vr[2];
+    auto load_v = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int key = kt + 2 * vkp + j;
+            vr[j] = key < a.kv_len
+                        ? *reinterpret_cast<const i32x4 *>(vbase + (int64_t)key * a.v_st + 16 * vc16)
+                        : i32x4{0, 0, 0, 0};
+        }
+    };
+    if (stager) load_v(kt0);
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
+    KTile<D> cur, nxt;
+    if (wt0 <= wt1) load_k_tile<D>(cur, kbase, a.k_st, wt0, a.kv_len, col, grp);
     for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
         __syncthreads();  // the previous tile's readers are done
-        for (int i = tid; i < kIntKeys * D / 16; i += kIntThreads) {
-            const int key = kt + i / (D / 16), c16 = i % (D / 16);
-            i32x4 w = {0, 0, 0, 0};
-            if (key < a.kv_len)
-                w = *reinterpret_cast<const i32x4 *>(vbase + (int64_t)key * a.v_st + 16 * c16);
-            *reinterpret_cast<i32x4 *>(sV + (key - kt) * D + 16 * c16) = w;
+        if (stager) {
+            const int8_t *b0 = reinterpret_cast<const int8_t *>(&vr[0]);
+            const int8_t *b1 = reinterpret_cast<const int8_t *>(&vr[1]);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+                const f16x2 pr = {(_Float16)(int16_t)b0[c], (_Float16)(int16_t)b1[c]};
+                *reinterpret_cast<f16x2 *>(sV + (16 * vc16 + c) * kVRow + 2 * vkp) = pr;
+            }
+            if (kt + kIntKeys <= key_hi) load_v(kt + kIntKeys);
         }
         __syncthreads();
-        if (!wave_needs(kt)) continue;
+        if (kt < wt0 || kt > wt1) continue;
+        const bool more = kt + kIntKeys <= wt1;
+        if (more) load_k_tile<D>(nxt, kbase, a.k_st, kt + kIntKeys, a.kv_len, col, grp);
+        const bool full = tile_full(kt);
+        const i32x16 s[2] = {tile_scores<D>(cur, 0, qop), tile_scores<D>(cur, 1, qop)};
         f16x8 pop[2][2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const i32x16 s = int_scores<D>(qop, kbase, a.k_st, kt + 32 * u, a.kv_len, col, grp);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                uint32_t p = 0;
-                if (visible(kt + 32 * u + 16 * grp + r)) {
-                    const uint32_t d = (uint32_t)((mx - s[r]) >> a.score_shift);
-                    const uint32_t scaled = (uint32_t)sTable[d < 255u ? d : 255u] * recip;
-                    p = (scaled >> 16) + ((scaled >> 15) & 1u);
-                    p = p < 255u ? p : 255u;
-                }
+                const uint32_t scaled = weight(s[u][r]) * recip;
+                uint32_t p = (scaled >> 16) + ((scaled >> 15) & 1u);
+                p = p < 255u ? p : 255u;
+                if (!full) p = visible(kt + 32 * u + 16 * grp + r) ? p : 0u;
                 pop[u][r >> 3][r & 7] = (_Float16)(float)p;
             }
         }
+        if (more) cur = nxt;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -187,9 +271,7 @@ __global__ __launch_bounds__(kIntThreads) void int_head_kernel(IntHeadArgs a) {
                 const int k0 = 32 * u + 16 * grp + 8 * s8;  // this lane's 8 keys in the tile
 #pragma unroll
                 for (int d = 0; d < DB; ++d) {
-                    f16x8 vop;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) vop[e] = (_Float16)(float)sV[(k0 + e) * D + 32 * d + col];
+                    const f16x8 vop = *reinterpret_cast<const f16x8 *>(sV + (32 * d + col) * kVRow + k0);
                     acc[d] = mfma_32x32x16_f16(vop, pop[u][s8], acc[d]);
                 }
             }
