@@ -23,6 +23,8 @@
 namespace reef {
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kIntThreads = 256;  // 4 waves x 32 query rows
 constexpr int kIntRows = 128;
 constexpr int kIntKeys = 64;  // keys per tile
@@ -87,6 +89,14 @@ __device__ __forceinline__ void for_k_tiles(int t0, int t1, const int8_t *kbase,
         if (kt + 2 * kIntKeys <= t1) load_k_tile<D>(ka, kbase, k_st, kt + 2 * kIntKeys, kv_len, col, grp);
         f(kt + kIntKeys, kb);
     }
+}
+
+// a * b + c for a, b < 2^24 (low 32 bits), one full-rate instruction; the compiler
+// otherwise picks a 64-bit multiply-add for this form.
+__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
 }
 
 __device__ __forceinline__ int32_t rounding_shift_dev(int32_t value, int shift) {
@@ -208,6 +218,8 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
     // The maximum's weight is the table's first entry, so sum > 0 on a row that
     // sees a key; rows outside the tensor never store.
     const uint32_t recip = sum > 0 ? (255u << 16) / sum : 0u;
+    const uint32_t recip24 = recip & 0xFFFFFFu;  // the same value (< 2^24)
+    const uint32_t half16 = 32768u;
 
     // Pass 3: probabilities and P.V (:218-227, 268-276). Thread i < 2 D stages
     // keys 2 (i % 32) and 2 (i % 32) + 1, channels 16 (i / 32) .. + 15 of each
@@ -230,9 +242,9 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
-    KTile<D> cur, nxt;
-    if (wt0 <= wt1) load_k_tile<D>(cur, kbase, a.k_st, wt0, a.kv_len, col, grp);
-    for (int kt = kt0; kt <= key_hi; kt += kIntKeys) {
+    // One value tile: stage it, then (for the wave's tiles) the probabilities and
+    // P.V with this tile's K operands kc while the next tile's load into kn.
+    auto tile3 = [&](int kt, const KTile<D> &kc, KTile<D> &kn) {
         __syncthreads();  // the previous tile's readers are done
         if (stager) {
             const int8_t *b0 = reinterpret_cast<const int8_t *>(&vr[0]);
@@ -246,24 +258,39 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
             if (kt + kIntKeys <= key_hi) load_v(kt + kIntKeys);
         }
         __syncthreads();
-        if (kt < wt0 || kt > wt1) continue;
-        const bool more = kt + kIntKeys <= wt1;
-        if (more) load_k_tile<D>(nxt, kbase, a.k_st, kt + kIntKeys, a.kv_len, col, grp);
+        if (kt < wt0 || kt > wt1) return;
+        if (kt + kIntKeys <= wt1) load_k_tile<D>(kn, kbase, a.k_st, kt + kIntKeys, a.kv_len, col, grp);
         const bool full = tile_full(kt);
-        const i32x16 s[2] = {tile_scores<D>(cur, 0, qop), tile_scores<D>(cur, 1, qop)};
+        const i32x16 s[2] = {tile_scores<D>(kc, 0, qop), tile_scores<D>(kc, 1, qop)};
+        // (scaled >> 16) + ((scaled >> 15) & 1) == (scaled + 2^15) >> 16. A visible
+        // key's w is one of the summed weights, so scaled = w * recip <= 255 << 16:
+        // a 24-bit product (v_mad_u32_u24), and p <= 255 (the engine's clamp never
+        // binds). Masked keys' products are discarded.
+        uint32_t pv[2][16];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pv[u][r] = mad_u24(weight(s[u][r]), recip24, half16) >> 16;
+        if (!full) {  // one uniform branch around all of the tile's selects
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    pv[u][r] = visible(kt + 32 * u + 16 * grp + r) ? pv[u][r] : 0u;
+        }
+        // p <= 255 to fp16, two at a time: 0x6400 | p is the fp16 bit pattern of
+        // 1024 + p, and one packed subtraction of 1024 leaves p exactly.
         f16x8 pop[2][2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t scaled = weight(s[u][r]) * recip;
-                uint32_t p = (scaled >> 16) + ((scaled >> 15) & 1u);
-                p = p < 255u ? p : 255u;
-                if (!full) p = visible(kt + 32 * u + 16 * grp + r) ? p : 0u;
-                pop[u][r >> 3][r & 7] = (_Float16)(float)p;
+            for (int hf = 0; hf < 2; ++hf) {
+                u32x4 bits;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    bits[e] = pv[u][8 * hf + 2 * e] | (pv[u][8 * hf + 2 * e + 1] << 16) | 0x64006400u;
+                pop[u][hf] = __builtin_bit_cast(f16x8, bits) - (f16x8)(_Float16)1024.0f;
             }
-        }
-        if (more) cur = nxt;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -275,6 +302,18 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
                     acc[d] = mfma_32x32x16_f16(vop, pop[u][s8], acc[d]);
                 }
             }
+    };
+    // Tiles alternate between the two K buffers by their index from kt0; the
+    // wave's first tile goes to the buffer of its parity.
+    KTile<D> ka, kb;
+    if (wt0 <= wt1) {
+        if (((wt0 - kt0) / kIntKeys) & 1) load_k_tile<D>(kb, kbase, a.k_st, wt0, a.kv_len, col, grp);
+        else load_k_tile<D>(ka, kbase, a.k_st, wt0, a.kv_len, col, grp);
+    }
+    for (int kt = kt0; kt <= key_hi; kt += 2 * kIntKeys) {
+        tile3(kt, ka, kb);
+        if (kt + kIntKeys > key_hi) break;
+        tile3(kt + kIntKeys, kb, ka);
     }
 
     if (!row_ok) return;
