@@ -9,10 +9,11 @@
 // The weights depend on the row's final maximum and the probabilities on the
 // final sum, so the keys are visited three times (maximum, sum, output), each
 // time recomputing the exact int32 scores on v_mfma_i32_32x32x32_i8 rather than
-// storing them (the next tile's K operands load while a tile is processed; tiles
-// that every row of a wave sees skip the per-key mask). p * v runs on
-// v_mfma_f32_32x32x16_f16 with the value tile staged once per workgroup as fp16
-// in channel-major rows (one 16-byte LDS read per operand): p <= 255 and v are exact
+// storing them. Each pass stages the key tiles in LDS once per workgroup (double
+// buffered, the next tile's loads in flight); tiles that every row of a wave sees
+// skip the per-key mask. p * v runs on v_mfma_f32_32x32x16_f16 with the value
+// tile staged as fp16 in channel-major rows (one 16-byte LDS read per operand):
+// p <= 255 and v are exact
 // in fp16, and every partial sum is an integer below 2^24 (at most 510 keys can
 // carry p > 0 beyond the ~255 the probabilities sum to, so |sum| <= 128 * 510),
 // so the fp32 accumulation is exact and the result is the engine's integer.
@@ -39,56 +40,11 @@ struct IntHeadArgs {
 };
 
 // Row m of a 32-key score block holds key 16 ((m >> 2) & 1) + 4 (m >> 3) + (m & 3),
-// so that output register r of lane group g is key 16 g + r.
-__device__ __forceinline__ int int_key_of_row(int m) {
-    return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
-}
-
-// K operands of one 64-key tile for this lane: block u (keys kt + 32 u ...), step
-// t of the head dimension. Row m of a block is key int_key_of_row(m); keys past
-// kv_len read key 0 (their scores are masked).
-template <int D>
-struct KTile {
-    i32x4 op[2][D / 32];
-};
-
-template <int D>
-__device__ __forceinline__ void load_k_tile(KTile<D> &k, const int8_t *kbase, int64_t k_st,
-                                            int kt, int kv_len, int col, int grp) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int key = kt + 32 * u + int_key_of_row(col);
-        const int8_t *krow = kbase + (int64_t)(key < kv_len ? key : 0) * k_st;
-#pragma unroll
-        for (int t = 0; t < D / 32; ++t)
-            k.op[u][t] = *reinterpret_cast<const i32x4 *>(krow + 32 * t + 16 * grp);
-    }
-}
-
-// Scores of 32-key block u for this lane's query: register r of lane group g is
-// key kt + 32 u + 16 g + r.
-template <int D>
-__device__ __forceinline__ i32x16 tile_scores(const KTile<D> &k, int u, const i32x4 (&qop)[D / 32]) {
-    i32x16 s = {};
-#pragma unroll
-    for (int t = 0; t < D / 32; ++t) s = mfma_32x32x32_i8(k.op[u][t], qop[t], s);
-    return s;
-}
-
-// f(kt, k) for the tiles kt = t0, t0 + 64, ..., t1 with their K operands, the next
-// tile's loads in flight while f runs (two buffers taken in turn, no copies).
-template <int D, typename F>
-__device__ __forceinline__ void for_k_tiles(int t0, int t1, const int8_t *kbase, int64_t k_st,
-                                            int kv_len, int col, int grp, F f) {
-    KTile<D> ka, kb;
-    if (t0 <= t1) load_k_tile<D>(ka, kbase, k_st, t0, kv_len, col, grp);
-    for (int kt = t0; kt <= t1; kt += 2 * kIntKeys) {
-        if (kt + kIntKeys <= t1) load_k_tile<D>(kb, kbase, k_st, kt + kIntKeys, kv_len, col, grp);
-        f(kt, ka);
-        if (kt + kIntKeys > t1) break;
-        if (kt + 2 * kIntKeys <= t1) load_k_tile<D>(ka, kbase, k_st, kt + 2 * kIntKeys, kv_len, col, grp);
-        f(kt + kIntKeys, kb);
-    }
+// so that output register r of lane group g is key 16 g + r. The K tile sits in
+// LDS in that row order: key kk of a block is stored at row
+// (kk & 3) | ((kk >> 4) & 1) << 2 | ((kk >> 2) & 3) << 3, the inverse map.
+__device__ __forceinline__ int int_row_of_key(int kk) {
+    return (kk & 3) | (((kk >> 4) & 1) << 2) | (((kk >> 2) & 3) << 3);
 }
 
 // a * b + c for a, b < 2^24 (low 32 bits), one full-rate instruction; the compiler
@@ -103,16 +59,28 @@ __device__ __forceinline__ int32_t rounding_shift_dev(int32_t value, int shift) 
     return shift == 0 ? value : (value >> shift) + ((value >> (shift - 1)) & 1);
 }
 
-// The value tile in LDS: fp16, channel-major (row c holds the tile's 64 keys of
-// channel c), rows padded to 72 halves so that the 16-byte operand reads of 8
-// consecutive channels fall in distinct banks.
-constexpr int kVRow = kIntKeys + 8;
+// LDS tiles, each double-buffered (tile j in buffer j & 1, one barrier per tile):
+// - K: rows of D bytes padded by 16, in the score blocks' row order, so that lane
+//   c's 16-byte operand read is row c and 8 consecutive lanes hit distinct banks;
+// - V (output pass only): fp16, channel-major (row c holds the tile's 64 keys of
+//   channel c), rows padded to 72 halves for the same reason.
+template <int D>
+struct IntLds {
+    static constexpr int K_ROW = D + 16;
+    static constexpr int K_BYTES = kIntKeys * K_ROW;
+    static constexpr int V_ROW = kIntKeys + 8;
+    static constexpr int V_BYTES = D * V_ROW * 2;
+    static constexpr int K_CHUNKS = kIntKeys * D / 16;  // 16-byte chunks per K tile
+    static constexpr int K_PER_THREAD = (K_CHUNKS + kIntThreads - 1) / kIntThreads;
+};
 
 template <int D>
 __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a) {
+    using L = IntLds<D>;
     constexpr int DB = D / 32;
     __shared__ uint16_t sTable[256];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[D * kVRow];
+    __shared__ __attribute__((aligned(16))) int8_t sK[2][L::K_BYTES];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][D * L::V_ROW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -157,19 +125,77 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
 
     const int8_t *kbase = a.k + b * a.k_sb + kvh * a.k_sh;
     const int8_t *vbase = a.v + b * a.v_sb + kvh * a.v_sh;
-    __syncthreads();  // the table
 
     // lo <= key <= hi as one unsigned compare (a select, not a branch)
     auto visible = [&](int key) { return (uint32_t)(key - lo) <= (uint32_t)(hi - lo); };
     // Every valid row of the wave sees every key of tile kt: no per-key mask.
     auto tile_full = [&](int kt) { return kt >= full_lo && kt + kIntKeys - 1 <= full_hi; };
 
+    // K staging: chunk i = tid + 256 j is key i / (D / 16), bytes 16 (i % (D / 16)).
+    i32x4 kr[L::K_PER_THREAD];
+    auto load_k = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < L::K_PER_THREAD; ++j) {
+            const int i = tid + kIntThreads * j;
+            const int key = kt + i / (D / 16);
+            kr[j] = i < L::K_CHUNKS && key < a.kv_len
+                        ? *reinterpret_cast<const i32x4 *>(kbase + (int64_t)key * a.k_st +
+                                                           16 * (i % (D / 16)))
+                        : i32x4{0, 0, 0, 0};
+        }
+    };
+    auto store_k = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < L::K_PER_THREAD; ++j) {
+            const int i = tid + kIntThreads * j;
+            const int kk = i / (D / 16);
+            if (i < L::K_CHUNKS)
+                *reinterpret_cast<i32x4 *>(
+                    &sK[buf][((kk & ~31) | int_row_of_key(kk & 31)) * L::K_ROW + 16 * (i % (D / 16))]) =
+                    kr[j];
+        }
+    };
+    // Scores of 32-key block u of the staged tile for this lane's query: register r
+    // of lane group g is key 32 u + 16 g + r (each lane reads the K row of its
+    // output column).
+    auto scores = [&](int buf, int u) {
+        const int8_t *krow = &sK[buf][(32 * u + col) * L::K_ROW + 16 * grp];
+        i32x16 s = {};
+#pragma unroll
+        for (int t = 0; t < DB; ++t)
+            s = mfma_32x32x32_i8(*reinterpret_cast<const i32x4 *>(krow + 32 * t), qop[t], s);
+        return s;
+    };
+    // Walk the workgroup's tiles: tile kt is staged in LDS (the next one's global
+    // loads in flight meanwhile), then f(kt, buf) runs for the wave's own tiles.
+    // extra_load(kt) / extra_store(buf) stage more per-tile data the same way.
+    auto walk = [&](auto f, auto extra_load, auto extra_store) {
+        load_k(kt0);
+        extra_load(kt0);
+        int buf = 0;
+        for (int kt = kt0; kt <= key_hi; kt += kIntKeys, buf ^= 1) {
+            store_k(buf);
+            extra_store(buf);
+            if (kt + kIntKeys <= key_hi) {
+                load_k(kt + kIntKeys);
+                extra_load(kt + kIntKeys);
+            }
+            // the stores are visible; every wave has finished reading this buffer's
+            // previous tile (it did so before the last barrier)
+            __syncthreads();
+            if (kt >= wt0 && kt <= wt1) f(kt, buf);
+        }
+        __syncthreads();  // the next walk's first stores reuse the buffers
+    };
+    auto no_load = [](int) {};
+    auto no_store = [](int) {};
+
     // The per-key work below is branch-free: a tile is either seen whole by every
     // row of the wave (wave-uniform test, no mask) or masked with selects.
     // Pass 1: the row maximum over visible keys (int8.hpp:197-203).
     int32_t mx = INT32_MIN;
-    for_k_tiles<D>(wt0, wt1, kbase, a.k_st, a.kv_len, col, grp, [&](int kt, const KTile<D> &k) {
-        const i32x16 s[2] = {tile_scores<D>(k, 0, qop), tile_scores<D>(k, 1, qop)};
+    walk([&](int kt, int buf) {
+        const i32x16 s[2] = {scores(buf, 0), scores(buf, 1)};
         if (tile_full(kt)) {
 #pragma unroll
             for (int u = 0; u < 2; ++u)
@@ -182,7 +208,7 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
                 for (int r = 0; r < 16; ++r)
                     mx = max(mx, visible(kt + 32 * u + 16 * grp + r) ? s[u][r] : INT32_MIN);
         }
-    });
+    }, no_load, no_store);
     {
         const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)mx, (uint32_t)mx, false, false);
         mx = max((int32_t)sw[0], (int32_t)sw[1]);
@@ -194,8 +220,8 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
         const uint32_t d = (uint32_t)((mx - sc) >> a.score_shift);
         return (uint32_t)sTable[d < 255u ? d : 255u];
     };
-    for_k_tiles<D>(wt0, wt1, kbase, a.k_st, a.kv_len, col, grp, [&](int kt, const KTile<D> &k) {
-        const i32x16 s[2] = {tile_scores<D>(k, 0, qop), tile_scores<D>(k, 1, qop)};
+    walk([&](int kt, int buf) {
+        const i32x16 s[2] = {scores(buf, 0), scores(buf, 1)};
         if (tile_full(kt)) {
 #pragma unroll
             for (int u = 0; u < 2; ++u)
@@ -210,7 +236,7 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
                     sum += visible(kt + 32 * u + 16 * grp + r) ? w : 0u;
                 }
         }
-    });
+    }, no_load, no_store);
     {
         const auto sw = __builtin_amdgcn_permlane32_swap(sum, sum, false, false);
         sum = sw[0] + sw[1];
@@ -221,15 +247,16 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
     const uint32_t recip24 = recip & 0xFFFFFFu;  // the same value (< 2^24)
     const uint32_t half16 = 32768u;
 
-    // Pass 3: probabilities and P.V (:218-227, 268-276). Thread i < 2 D stages
+    // Pass 3: probabilities and P.V (:218-227, 268-276). Thread i < 2 D also stages
     // keys 2 (i % 32) and 2 (i % 32) + 1, channels 16 (i / 32) .. + 15 of each
-    // value tile: 16-byte loads one tile ahead, converted exactly to fp16 and
-    // stored as key pairs into the channel-major LDS tile. Each lane then reads
-    // its 8 keys of one channel as one 16-byte operand.
+    // value tile, converted exactly to fp16 and stored as key pairs into the
+    // channel-major tile. Each lane then reads its 8 keys of one channel as one
+    // 16-byte operand.
     const bool stager = tid < 2 * D;
     const int vkp = tid % 32, vc16 = tid / 32;
     i32x4 vr[2];
     auto load_v = [&](int kt) {
+        if (!stager) return;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int key = kt + 2 * vkp + j;
@@ -238,30 +265,23 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
                         : i32x4{0, 0, 0, 0};
         }
     };
-    if (stager) load_v(kt0);
+    auto store_v = [&](int buf) {
+        if (!stager) return;
+        const int8_t *b0 = reinterpret_cast<const int8_t *>(&vr[0]);
+        const int8_t *b1 = reinterpret_cast<const int8_t *>(&vr[1]);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+            const f16x2 pr = {(_Float16)(int16_t)b0[c], (_Float16)(int16_t)b1[c]};
+            *reinterpret_cast<f16x2 *>(&sV[buf][(16 * vc16 + c) * L::V_ROW + 2 * vkp]) = pr;
+        }
+    };
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
-    // One value tile: stage it, then (for the wave's tiles) the probabilities and
-    // P.V with this tile's K operands kc while the next tile's load into kn.
-    auto tile3 = [&](int kt, const KTile<D> &kc, KTile<D> &kn) {
-        __syncthreads();  // the previous tile's readers are done
-        if (stager) {
-            const int8_t *b0 = reinterpret_cast<const int8_t *>(&vr[0]);
-            const int8_t *b1 = reinterpret_cast<const int8_t *>(&vr[1]);
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-                const f16x2 pr = {(_Float16)(int16_t)b0[c], (_Float16)(int16_t)b1[c]};
-                *reinterpret_cast<f16x2 *>(sV + (16 * vc16 + c) * kVRow + 2 * vkp) = pr;
-            }
-            if (kt + kIntKeys <= key_hi) load_v(kt + kIntKeys);
-        }
-        __syncthreads();
-        if (kt < wt0 || kt > wt1) return;
-        if (kt + kIntKeys <= wt1) load_k_tile<D>(kn, kbase, a.k_st, kt + kIntKeys, a.kv_len, col, grp);
+    walk([&](int kt, int buf) {
         const bool full = tile_full(kt);
-        const i32x16 s[2] = {tile_scores<D>(kc, 0, qop), tile_scores<D>(kc, 1, qop)};
+        const i32x16 s[2] = {scores(buf, 0), scores(buf, 1)};
         // (scaled >> 16) + ((scaled >> 15) & 1) == (scaled + 2^15) >> 16. A visible
         // key's w is one of the summed weights, so scaled = w * recip <= 255 << 16:
         // a 24-bit product (v_mad_u32_u24), and p <= 255 (the engine's clamp never
@@ -291,6 +311,7 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
                     bits[e] = pv[u][8 * hf + 2 * e] | (pv[u][8 * hf + 2 * e + 1] << 16) | 0x64006400u;
                 pop[u][hf] = __builtin_bit_cast(f16x8, bits) - (f16x8)(_Float16)1024.0f;
             }
+        const _Float16 *vt = &sV[buf][col * L::V_ROW];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -298,23 +319,11 @@ __global__ __launch_bounds__(kIntThreads, 2) void int_head_kernel(IntHeadArgs a)
                 const int k0 = 32 * u + 16 * grp + 8 * s8;  // this lane's 8 keys in the tile
 #pragma unroll
                 for (int d = 0; d < DB; ++d) {
-                    const f16x8 vop = *reinterpret_cast<const f16x8 *>(sV + (32 * d + col) * kVRow + k0);
+                    const f16x8 vop = *reinterpret_cast<const f16x8 *>(vt + 32 * d * L::V_ROW + k0);
                     acc[d] = mfma_32x32x16_f16(vop, pop[u][s8], acc[d]);
                 }
             }
-    };
-    // Tiles alternate between the two K buffers by their index from kt0; the
-    // wave's first tile goes to the buffer of its parity.
-    KTile<D> ka, kb;
-    if (wt0 <= wt1) {
-        if (((wt0 - kt0) / kIntKeys) & 1) load_k_tile<D>(kb, kbase, a.k_st, wt0, a.kv_len, col, grp);
-        else load_k_tile<D>(ka, kbase, a.k_st, wt0, a.kv_len, col, grp);
-    }
-    for (int kt = kt0; kt <= key_hi; kt += 2 * kIntKeys) {
-        tile3(kt, ka, kb);
-        if (kt + kIntKeys > key_hi) break;
-        tile3(kt + kIntKeys, kb, ka);
-    }
+    }, load_v, store_v);
 
     if (!row_ok) return;
     // acc[d][4j + i] is channel 32 d + 8 j + 4 grp + i of this lane's row.
