@@ -32,32 +32,43 @@ struct AppendArgs {
     uint32_t *status;
 };
 
-// Largest |x| of the wave's row as IEEE bits (a NaN has the largest bits).
+// Largest |x| as IEEE bits (a NaN has the largest bits).
 __device__ __forceinline__ uint32_t mag(float x) { return __float_as_uint(x) & 0x7fffffffu; }
 
-// Quantizes the row of D values at src (lane holds channels lane + 64 j) and
-// stores the codes through store(d, code); returns the scale.
-template <int D, typename Store>
-__device__ __forceinline__ float quantize_row(const float *src, int lane, bool &bad, Store store) {
-    constexpr int PER = D / kWave;
-    float x[PER];
-    uint32_t m = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        x[j] = src[lane + kWave * j];
-        const uint32_t b = mag(x[j]);
-        m = m > b ? m : b;
-    }
-    m = wave_max_u32(m);
-    bad = m >= 0x7f800000u;
-    const float scale = int8_scale(__uint_as_float(m));
-#pragma unroll
-    for (int j = 0; j < PER; ++j) store(lane + kWave * j, quantize_int8(x[j], scale));
-    return scale;
+// Largest v over the LPR (8 or 16) lanes of this lane's group, in every lane of it:
+// a group is (part of) one 16-lane DPP row, reduced by the quad swaps, the mirrored
+// half row and (16 lanes) the mirrored row.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_max(uint32_t v) {
+    const uint32_t w = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+    return v > w ? v : w;
 }
 
-template <int D, bool PAGED>
+template <int LPR>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+    v = dpp_max<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v = dpp_max<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v = dpp_max<0x141>(v);  // row_half_mirror
+    if (LPR == 16) v = dpp_max<0x140>(v);  // row_mirror
+    return v;
+}
+
+// Each wave quantizes 8 rows of the page (quantize_rows, quant.hpp:112-133): waves 0
+// and 1 the keys of slots 0-7 and 8-15, waves 2 and 3 the values. A row is spread
+// over LPR = D / 8 lanes holding 8 consecutive channels each, so a wave takes
+// 64 / LPR rows at once and a row's maximum is a reduction within a DPP row.
+//
+// The codes are rint(x / scale) clamped to +-127 with the engine's IEEE quotient,
+// computed as y = x * rcp(scale): the quotient t satisfies |t| <= 127 (1 + 2^-24)
+// since |x| <= max, rcp is within 1 ulp, and the product is rounded once, so
+// |y - t| < 2^-15.4, and t's own rounding adds under 2^-16.9: y lies within 3.1e-5
+// of the IEEE quotient. Unless y is within 2^-14 of a half-integer, rint(y) is the
+// engine's code. When any lane of the wave has such a value (rare: about 1.2e-4
+// per value), or a row is not finite or its scale is tiny, the wave redoes the
+// pass with IEEE divisions.
+template <int D, bool PAGED, bool VEC>
 __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
+    constexpr int LPR = D / 8, RPW = kWave / LPR, PASSES = 8 / RPW;
     __shared__ __attribute__((aligned(16))) int8_t sK[kPage * D];   // [slot][channel]
     __shared__ __attribute__((aligned(16))) int8_t sVT[D * kPage];  // [channel][slot]
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -86,26 +97,76 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
     } else {
         page_base = ((int64_t)b * a.kv_heads + kvh) * (a.max_context / kPage) + page_idx;
     }
-    // Wave w quantizes slots w, w + 4, w + 8, w + 12 of the page.
+    const bool is_v = wave >= 2;  // wave-uniform
+    const float *src = is_v ? a.v + b * a.v_sb + kvh * a.v_sh : a.k + b * a.k_sb + kvh * a.k_sh;
+    const int64_t st = is_v ? a.v_st : a.k_st;
+    float *scale_dst = (is_v ? a.vs_dst : a.ks_dst) + page_base * kPage;
+    const int g = lane / LPR, li = lane % LPR;
     bool bad = false;
 #pragma unroll
-    for (int i = 0; i < kPage / kAppendWaves; ++i) {
-        const int slot = wave + kAppendWaves * i;
+    for (int pass = 0; pass < PASSES; ++pass) {
+        const int slot = 8 * (wave & 1) + RPW * pass + g;
         const int pos = page_idx * kPage + slot;
-        if (pos < p_lo || pos >= p_hi) continue;  // wave-uniform
-        const int t = pos - start;
-        bool bad_k, bad_v;
-        const float ks = quantize_row<D>(a.k + b * a.k_sb + kvh * a.k_sh + (int64_t)t * a.k_st,
-                                         lane, bad_k, [&](int d, int8_t c) { sK[slot * D + d] = c; });
-        const float vs = quantize_row<D>(a.v + b * a.v_sb + kvh * a.v_sh + (int64_t)t * a.v_st,
-                                         lane, bad_v, [&](int d, int8_t c) { sVT[d * kPage + slot] = c; });
-        if (lane == 0) {
-            a.ks_dst[page_base * kPage + slot] = ks;
-            a.vs_dst[page_base * kPage + slot] = vs;
+        const bool valid = pos >= p_lo && pos < p_hi;
+        if (__builtin_amdgcn_ballot_w64(valid) == 0) continue;  // wave-uniform
+        float x[8];
+        if (valid) {
+            const float *row = src + (int64_t)(pos - start) * st + 8 * li;
+            if (VEC) {
+                const f32x4 lo4 = *reinterpret_cast<const f32x4 *>(row);
+                const f32x4 hi4 = *reinterpret_cast<const f32x4 *>(row + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[j] = lo4[j];
+                    x[4 + j] = hi4[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = row[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = 0.0f;
         }
-        bad |= bad_k || bad_v;
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = m > mag(x[j]) ? m : mag(x[j]);
+        m = group_max_u32<LPR>(m);
+        const bool row_bad = m >= 0x7f800000u;
+        const float scale = int8_scale(__uint_as_float(m));
+        const float rs = __builtin_amdgcn_rcpf(scale);
+        bool near = row_bad || !(scale >= 0x1p-125f);
+        float qf[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float y = x[j] * rs;
+            qf[j] = __builtin_rintf(y);
+            near |= __builtin_fabsf(y - qf[j]) > 0.5f - 0x1p-14f;
+        }
+        if (__builtin_amdgcn_ballot_w64(near && valid) != 0) {  // rare: IEEE quotients
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qf[j] = __builtin_rintf(x[j] / scale);
+        }
+        uint32_t c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float r = qf[j] < -127.0f ? -127.0f : (qf[j] > 127.0f ? 127.0f : qf[j]);
+            c[j] = (uint32_t)(int32_t)r & 0xffu;
+        }
+        if (valid) {
+            bad |= row_bad;
+            if (is_v) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sVT[(8 * li + j) * kPage + slot] = (int8_t)c[j];
+            } else {
+                const uint32_t w0 = c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24;
+                const uint32_t w1 = c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24;
+                *reinterpret_cast<uint2 *>(sK + slot * D + 8 * li) = make_uint2(w0, w1);
+            }
+            if (li == 0) scale_dst[slot] = scale;
+        }
     }
-    if (bad && lane == 0) flag_status(a.status, REEF_STATUS_BIT_NON_FINITE);
+    if (bad) flag_status(a.status, REEF_STATUS_BIT_NON_FINITE);
     __syncthreads();
     int8_t *kpage = a.k_dst + page_base * kPage * D;
     int8_t *vpage = a.v_dst + page_base * D * kPage;
@@ -186,10 +247,16 @@ reef_status launch(const reef_kv_append_params *p, AppendArgs &a, int32_t *conte
     // starts inside a page
     const dim3 grid((unsigned)(ceil_div(p->new_tokens, kPage) + 1), (unsigned)p->kv_heads,
                     (unsigned)p->batch);
-    if (p->head_dim == 128)
-        hipLaunchKernelGGL((kv_append<128, PAGED>), grid, dim3(kAppendThreads), 0, stream, a);
-    else
-        hipLaunchKernelGGL((kv_append<64, PAGED>), grid, dim3(kAppendThreads), 0, stream, a);
+    // 16-byte row loads when every new row starts 16-byte aligned
+    const bool vec = aligned(a.k, 16) && aligned(a.v, 16) && a.k_sb % 4 == 0 && a.k_sh % 4 == 0 &&
+                     a.k_st % 4 == 0 && a.v_sb % 4 == 0 && a.v_sh % 4 == 0 && a.v_st % 4 == 0;
+    if (p->head_dim == 128) {
+        if (vec) hipLaunchKernelGGL((kv_append<128, PAGED, true>), grid, dim3(kAppendThreads), 0, stream, a);
+        else hipLaunchKernelGGL((kv_append<128, PAGED, false>), grid, dim3(kAppendThreads), 0, stream, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((kv_append<64, PAGED, true>), grid, dim3(kAppendThreads), 0, stream, a);
+        else hipLaunchKernelGGL((kv_append<64, PAGED, false>), grid, dim3(kAppendThreads), 0, stream, a);
+    }
     if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
     if (context_lens) {
         hipLaunchKernelGGL(advance_lengths, dim3((unsigned)ceil_div(p->batch, 256)), dim3(256), 0,

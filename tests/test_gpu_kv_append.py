@@ -103,6 +103,37 @@ def test_append_from_projection_layout_and_ragged_starts(reef):
     assert np.array_equal(host(dks).view(np.uint32), ks.view(np.uint32))
 
 
+@pytest.mark.parametrize("D,offset", [(128, 0), (128, 1), (64, 1)])
+def test_append_ties_and_unaligned_rows(reef, D, offset):
+    """Rows whose scale is exactly 1 (largest magnitude 127) with half-integer values:
+    x / scale is a tie, so the kernel's reciprocal product lands on the half-integer
+    and the wave redoes the row with IEEE divisions (ties to even). offset 1 shifts
+    the rows by one float, so they are not 16-byte aligned (scalar loads)."""
+    case(f"kv_append ties D{D} offset{offset}")
+    B, H, L, T = 2, 2, 48, 20
+    k, v, ks, vs = empty_cache(B, H, L, D)
+    dk, dv, dks, dvs = gpu(k), gpu(v), gpu(ks), gpu(vs)
+    rng = np.random.default_rng(D + offset)
+    kf = (rng.integers(-254, 255, (B, H, T, D)) / 2.0).astype(np.float32)
+    kf[:, :, :, 0] = 127.0
+    vf = W.lcg_normal(9, B * H * T * D).reshape(B, H, T, D)
+    vf[:, :, ::2, 3] = -127.0
+    vf[:, :, ::2, 4:12] = np.array([2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 126.5, -1.5], np.float32)
+    starts = np.array([5, 16], np.int32)
+
+    def shifted(a):
+        flat = torch.zeros(a.size + offset, dtype=torch.float32, device="cuda")
+        flat[offset:] = torch.from_numpy(a.ravel()).cuda()
+        return flat[offset:].view(a.shape)
+    reef.kv_append(shifted(kf), shifted(vf), gpu(starts), dk, dv, dks, dvs)
+    for b in range(B):
+        expect_rows(k, v, ks, vs, b, int(starts[b]), kf[b], vf[b])
+    assert np.array_equal(host(dk), k)
+    assert np.array_equal(host(dv), v)
+    assert np.array_equal(host(dks).view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(host(dvs).view(np.uint32), vs.view(np.uint32))
+
+
 def test_append_capacity_and_non_finite(reef):
     case("kv_append: capacity exceeded for one sequence; non-finite rows")
     B, H, L, D, T = 2, 1, 32, 64, 4
