@@ -102,35 +102,43 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
     const int64_t st = is_v ? a.v_st : a.k_st;
     float *scale_dst = (is_v ? a.vs_dst : a.ks_dst) + page_base * kPage;
     const int g = lane / LPR, li = lane % LPR;
-    bool bad = false;
+    // Every pass's loads are issued before any row is reduced.
+    float x[PASSES][8];
+    bool valid[PASSES];
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass) {
         const int slot = 8 * (wave & 1) + RPW * pass + g;
         const int pos = page_idx * kPage + slot;
-        const bool valid = pos >= p_lo && pos < p_hi;
-        if (__builtin_amdgcn_ballot_w64(valid) == 0) continue;  // wave-uniform
-        float x[8];
-        if (valid) {
-            const float *row = src + (int64_t)(pos - start) * st + 8 * li;
-            if (VEC) {
-                const f32x4 lo4 = *reinterpret_cast<const f32x4 *>(row);
-                const f32x4 hi4 = *reinterpret_cast<const f32x4 *>(row + 4);
+        valid[pass] = pos >= p_lo && pos < p_hi;
+        // rows outside the page's new range read new token 0 (always present) and
+        // are zeroed afterwards: the loads need no branch
+        const float *row = src + (int64_t)(valid[pass] ? pos - start : 0) * st + 8 * li;
+        if (VEC) {
+            const f32x4 lo4 = *reinterpret_cast<const f32x4 *>(row);
+            const f32x4 hi4 = *reinterpret_cast<const f32x4 *>(row + 4);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[j] = lo4[j];
-                    x[4 + j] = hi4[j];
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = row[j];
+            for (int j = 0; j < 4; ++j) {
+                x[pass][j] = lo4[j];
+                x[pass][4 + j] = hi4[j];
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+            for (int j = 0; j < 8; ++j) x[pass][j] = row[j];
         }
+    }
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[pass][j] = valid[pass] ? x[pass][j] : 0.0f;
+    }
+    bool bad = false;
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+        const int slot = 8 * (wave & 1) + RPW * pass + g;
+        if (__builtin_amdgcn_ballot_w64(valid[pass]) == 0) continue;  // wave-uniform
         uint32_t m = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) m = m > mag(x[j]) ? m : mag(x[j]);
+        for (int j = 0; j < 8; ++j) m = m > mag(x[pass][j]) ? m : mag(x[pass][j]);
         m = group_max_u32<LPR>(m);
         const bool row_bad = m >= 0x7f800000u;
         const float scale = int8_scale(__uint_as_float(m));
@@ -139,13 +147,13 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
         float qf[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float y = x[j] * rs;
+            const float y = x[pass][j] * rs;
             qf[j] = __builtin_rintf(y);
             near |= __builtin_fabsf(y - qf[j]) > 0.5f - 0x1p-14f;
         }
-        if (__builtin_amdgcn_ballot_w64(near && valid) != 0) {  // rare: IEEE quotients
+        if (__builtin_amdgcn_ballot_w64(near && valid[pass]) != 0) {  // rare: IEEE quotients
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qf[j] = __builtin_rintf(x[j] / scale);
+            for (int j = 0; j < 8; ++j) qf[j] = __builtin_rintf(x[pass][j] / scale);
         }
         uint32_t c[8];
 #pragma unroll
@@ -153,7 +161,7 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
             const float r = qf[j] < -127.0f ? -127.0f : (qf[j] > 127.0f ? 127.0f : qf[j]);
             c[j] = (uint32_t)(int32_t)r & 0xffu;
         }
-        if (valid) {
+        if (valid[pass]) {
             bad |= row_bad;
             if (is_v) {
 #pragma unroll
