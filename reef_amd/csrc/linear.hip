@@ -15,6 +15,7 @@
 // tiles sharing their input rows in that XCD's L2.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "reef_common.hpp"
 
@@ -61,26 +62,25 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
     return c ^ ((r / rows256) & (kChunks - 1));
 }
 
-__global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t smem[kStages][kABytes + kBBytes];  // [stage] A, B
+// One BM x BM output tile at (m0, n0) (BM = 128 or 64): 4 waves in a 2 x 2 grid,
+// each wave BM/2 x BM/2 in 32 x 32 blocks; the operand tiles of one stage are
+// BM x kBK (A) then BM x kBK (B) from the start of `smem`'s stage.
+template <int BM>
+__device__ __forceinline__ void gemm_tile(const GemmArgs &a, int m0, int n0,
+                                          int8_t (*smem)[kABytes + kBBytes]) {
+    constexpr int NBLK = BM / 64;                      // 32-wide blocks per wave and side
+    constexpr int TBYTES = BM * kBK;                   // one operand tile of a stage
+    constexpr int PA = TBYTES / 1024 / 4, PB = PA;     // 1 KB blocks per wave and operand
+    static_assert(PA >= 1 && 2 * TBYTES <= kABytes + kBBytes, "tile fits a stage");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int col = lane & 31, grp = lane >> 5;
 
-    // Workgroup i runs on XCD i % 8; give XCD x the contiguous tiles
-    // [start(x), start(x) + count(x)), tiles along `out` fastest.
-    const int T = (int)gridDim.x, g = (int)blockIdx.x;
-    const int x = g % kXcds, per = T / kXcds, rem = T % kXcds;
-    const int t = x * per + min(x, rem) + g / kXcds;
-    const int tm = t / a.n_tiles, tn = t % a.n_tiles;
-    const int m0 = tm * kBM, n0 = tn * kBN;
-
     // Direct loads: wave w fills 1 KB blocks w, w + 4, ... of each operand tile;
     // lane L of block b writes tile row kRowsPerBlock b + L / kChunks at position
     // L % kChunks, which holds chunk chunk_pos(row, L % kChunks). Rows past the end
     // and chunks past `in` read zeros: their offset is set beyond the buffer.
-    constexpr int PA = kABytes / 1024 / 4, PB = kBBytes / 1024 / 4;  // blocks per wave
     const uint32_t xbytes = (uint32_t)((int64_t)a.rows * a.in);
     const uint32_t wbytes = (uint32_t)((int64_t)a.out * a.in);
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, xbytes);
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a) 
     auto issue = [&](int s) {  // K step s (clamped to the last) into stage s % kStages
         const int k0 = min(s, steps - 1) * kBK;
         int8_t *sa = smem[s % kStages];
-        int8_t *sb = sa + kABytes;
+        int8_t *sb = sa + TBYTES;
         const bool in_k = k0 + kch < a.in;
 #pragma unroll
         for (int i = 0; i < PA; ++i)
@@ -116,18 +116,18 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a) 
                 in_k ? boff[i] : wbytes, k0, 0, 0);
     };
 
-    // Operand reads: row 64 wm + 32 i + col (A) or 32 (kNB wn + j) + col (B), chunk
-    // 2 ks + grp; the swizzle depends on bits 2-3 of the row, i.e. of col.
+    // Operand reads: row (BM/2) wm + 32 i + col (A) or (BM/2) wn + 32 j + col (B),
+    // chunk 2 ks + grp; the swizzle depends on bits 2-3 of the row, i.e. of col.
     int rpos[kBK / 32];
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ++ks) rpos[ks] = 16 * chunk_pos(col, 2 * ks + grp);
-    const int arow = (64 * wm + col) * kBK, brow = (32 * kNB * wn + col) * kBK;
+    const int arow = ((BM / 2) * wm + col) * kBK, brow = ((BM / 2) * wn + col) * kBK;
 
-    i32x16 acc[2][kNB];
+    i32x16 acc[NBLK][NBLK];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NBLK; ++i)
 #pragma unroll
-        for (int j = 0; j < kNB; ++j) acc[i][j] = i32x16{};
+        for (int j = 0; j < NBLK; ++j) acc[i][j] = i32x16{};
 
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s) issue(s);
@@ -145,40 +145,40 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a) 
         __builtin_amdgcn_s_barrier();
         issue(k + kStages - 1);
         const int8_t *sa = smem[k % kStages];
-        const int8_t *sb = sa + kABytes;
+        const int8_t *sb = sa + TBYTES;
 #pragma unroll
         for (int ks = 0; ks < kBK / 32; ++ks) {
-            i32x4 aop[2], bop[kNB];
+            i32x4 aop[NBLK], bop[NBLK];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NBLK; ++i)
                 aop[i] = *reinterpret_cast<const i32x4 *>(sa + arow + 32 * i * kBK + rpos[ks]);
 #pragma unroll
-            for (int j = 0; j < kNB; ++j)
+            for (int j = 0; j < NBLK; ++j)
                 bop[j] = *reinterpret_cast<const i32x4 *>(sb + brow + 32 * j * kBK + rpos[ks]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NBLK; ++i)
 #pragma unroll
-                for (int j = 0; j < kNB; ++j) acc[i][j] = mfma_32x32x32_i8(aop[i], bop[j], acc[i][j]);
+                for (int j = 0; j < NBLK; ++j) acc[i][j] = mfma_32x32x32_i8(aop[i], bop[j], acc[i][j]);
         }
     }
     // The trailing loads of the clamped last steps must land before the workgroup's
     // LDS can be handed to another workgroup.
     __builtin_amdgcn_s_waitcnt(0xf70);
 
-    // Epilogue: lane holds output column n0 + 32 (kNB wn + j) + col and, in register
-    // 4 q + e, row m0 + 64 wm + 32 i + 8 q + 4 grp + e.
+    // Epilogue: lane holds output column n0 + (BM/2) wn + 32 j + col and, in
+    // register 4 q + e, row m0 + (BM/2) wm + 32 i + 8 q + 4 grp + e.
     bool bad = false;
 #pragma unroll
-    for (int j = 0; j < kNB; ++j) {
-        const int n = n0 + 32 * (kNB * wn + j) + col;
+    for (int j = 0; j < NBLK; ++j) {
+        const int n = n0 + (BM / 2) * wn + 32 * j + col;
         if (n >= a.out) continue;
         const float wsc = a.ws[n];
         const float bn = a.bias ? a.bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < NBLK; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * grp + (r & 3);
+                const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (r >> 2) + 4 * grp + (r & 3);
                 if (m >= a.rows) continue;
                 float v;
                 {
@@ -192,6 +192,31 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a) 
             }
     }
     if (bad) flag_status(a.status, REEF_STATUS_BIT_OVERFLOW);
+}
+
+// Workgroups [0, n_big) take the 128 x 128 tiles [0, n_big) in tile order (tiles
+// along `out` fastest); when there are a few more tiles than compute units, the
+// remaining tiles are cut into four 64 x 64 quadrants, one workgroup each, so that
+// every compute unit holds one large tile and at most one quadrant instead of some
+// holding two large tiles while the others idle. Workgroup i runs on XCD
+// i % 8: each XCD gets a contiguous run of the large tiles and of the quadrants.
+__global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a, int n_big) {
+    static_assert(kBN == kBM, "square tiles");
+    __shared__ __attribute__((aligned(16))) int8_t smem[kStages][kABytes + kBBytes];  // [stage] A, B
+    const int g = (int)blockIdx.x;
+    auto xcd_rank = [](int i, int count) {
+        const int x = i % kXcds, per = count / kXcds, rem = count % kXcds;
+        return x * per + min(x, rem) + i / kXcds;
+    };
+    if (g < n_big) {
+        const int t = xcd_rank(g, n_big);
+        gemm_tile<kBM>(a, t / a.n_tiles * kBM, t % a.n_tiles * kBM, smem);
+    } else {
+        const int s = xcd_rank(g - n_big, (int)gridDim.x - n_big);
+        const int t = n_big + s / 4, q = s % 4;
+        gemm_tile<kBM / 2>(a, t / a.n_tiles * kBM + (kBM / 2) * (q >> 1),
+                           t % a.n_tiles * kBM + (kBM / 2) * (q & 1), smem);
+    }
 }
 
 reef_status launch_gemm(const int8_t *xq, const float *xs, int64_t rows, int64_t in,
@@ -212,7 +237,18 @@ reef_status launch_gemm(const int8_t *xq, const float *xs, int64_t rows, int64_t
     a.m_tiles = (int32_t)ceil_div(rows, kBM);
     a.status = status;
     const int64_t tiles = (int64_t)a.m_tiles * a.n_tiles;
-    hipLaunchKernelGGL(gemm_w8a8_kernel, dim3((unsigned)tiles), dim3(kGemmThreads), 0, stream, a);
+    // Up to a quarter more tiles than compute units: the tiles past one per unit go
+    // as quadrants, so the grid is at most two workgroups per unit (measured on
+    // 4096 x 8192 -> 1280, 320 tiles: 64.5 us against 70.4; with more tiles the
+    // extra quadrants queue and it loses: 384 tiles 84.9 against 80.7 us).
+    // REEF_GEMM_QUADRANTS=0 turns this off.
+    const int64_t cus = compute_units();
+    const char *env = getenv("REEF_GEMM_QUADRANTS");
+    const bool quads = (env ? atoi(env) != 0 : true) && tiles > cus && 4 * (tiles - cus) <= cus;
+    const int64_t n_big = quads ? cus : tiles;
+    const int64_t grid = n_big + 4 * (tiles - n_big);
+    hipLaunchKernelGGL(gemm_w8a8_kernel, dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, a,
+                       (int)n_big);
     return launch_status();
 }
 

@@ -98,3 +98,22 @@ def test_linear_errors(reef):
         reef.linear_w8a8(gpu(np.ones((4, 30), np.float32)), gpu(np.ones((8, 30), np.int8)), gpu(ws))
     y = host(reef.linear_w8a8(gpu(x), gpu(w), gpu(ws)))  # the status word is clean again
     assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("quadrants", ["1", "0"])
+def test_linear_quadrant_tiles(reef, quadrants, monkeypatch):
+    """2000 x 256 -> 2500: 16 x 20 = 320 output tiles of 128 x 128, between one and
+    two per compute unit, so the tiles past the first 256 run as four 64 x 64
+    quadrants each (including the ragged last row and column of tiles). Bit-exact
+    against the oracle with the quadrants and with whole tiles only."""
+    monkeypatch.setenv("REEF_GEMM_QUADRANTS", quadrants)
+    rows, fin, fout = 2000, 256, 2500
+    case(f"w8a8 rows{rows} in{fin} out{fout} quadrants={quadrants}")
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((rows, fin)).astype(np.float32)
+    w = rng.integers(-127, 128, (fout, fin), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.02, fout).astype(np.float32)
+    b = rng.standard_normal(fout).astype(np.float32)
+    y = host(reef.linear_w8a8(gpu(x), gpu(w), gpu(ws), gpu(b)))
+    gold = oracle_linear(x, w, ws, b)
+    assert np.array_equal(y.view(np.uint32), gold.view(np.uint32))
