@@ -6,10 +6,10 @@
 // is preallocated to its capacity and stays in place. One workgroup fills one
 // 16-token cache page of one (sequence, KV head) with the new tokens that fall
 // in it: each wave quantizes key and value rows (quantize_rows,
-// quant.hpp:112-133, bit-identical codes and scales) into LDS, K token-major and
-// V already transposed, and the page then leaves in 16-byte stores, whole pages
-// as they are laid out in the cache (K [16, D], V [D, 16], the layout the decode
-// kernel reads). The capacity check of attention.hpp:321-327 becomes a status
+// quant.hpp:112-133, bit-identical codes and scales) into token-major LDS
+// images, and the page then leaves in 16-byte stores, whole pages as they are
+// laid out in the cache (K [16, D], V transposed to [D, 16] on the way out: the
+// layout the decode kernel reads). The capacity check of attention.hpp:321-327 becomes a status
 // bit, since the lengths live on the device.
 #include "reef_common.hpp"
 
@@ -69,8 +69,10 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
 template <int D, bool PAGED, bool VEC>
 __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
     constexpr int LPR = D / 8, RPW = kWave / LPR, PASSES = 8 / RPW;
-    __shared__ __attribute__((aligned(16))) int8_t sK[kPage * D];   // [slot][channel]
-    __shared__ __attribute__((aligned(16))) int8_t sVT[D * kPage];  // [channel][slot]
+    // Both images token-major ([slot][channel]): 8-byte code writes with no bank
+    // conflicts. The value page is transposed to [channel][slot] as it is stored.
+    __shared__ __attribute__((aligned(16))) int8_t sK[kPage * D];
+    __shared__ __attribute__((aligned(16))) int8_t sV[kPage * D];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.z, kvh = blockIdx.y;
@@ -163,14 +165,9 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
         }
         if (valid[pass]) {
             bad |= row_bad;
-            if (is_v) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) sVT[(8 * li + j) * kPage + slot] = (int8_t)c[j];
-            } else {
-                const uint32_t w0 = c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24;
-                const uint32_t w1 = c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24;
-                *reinterpret_cast<uint2 *>(sK + slot * D + 8 * li) = make_uint2(w0, w1);
-            }
+            const uint32_t w0 = c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24;
+            const uint32_t w1 = c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24;
+            *reinterpret_cast<uint2 *>((is_v ? sV : sK) + slot * D + 8 * li) = make_uint2(w0, w1);
             if (li == 0) scale_dst[slot] = scale;
         }
     }
@@ -179,10 +176,22 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
     int8_t *kpage = a.k_dst + page_base * kPage * D;
     int8_t *vpage = a.v_dst + page_base * D * kPage;
     if (p_hi - p_lo == kPage) {
-        // A whole page: 16-byte copies of both LDS images.
-        for (int o = 16 * tid; o < kPage * D; o += 16 * kAppendThreads) {
-            *reinterpret_cast<i32x4 *>(kpage + o) = *reinterpret_cast<const i32x4 *>(sK + o);
-            *reinterpret_cast<i32x4 *>(vpage + o) = *reinterpret_cast<const i32x4 *>(sVT + o);
+        // A whole page: threads [0, D) copy the key image in 16-byte chunks; thread
+        // 128 + c gathers channel c's 16 slots of the value image (consecutive lanes
+        // read consecutive bytes) into the transposed page row [c][0..15].
+        if (tid < kPage * D / 16) {
+            *reinterpret_cast<i32x4 *>(kpage + 16 * tid) = *reinterpret_cast<const i32x4 *>(sK + 16 * tid);
+        } else if (tid >= 128 && tid < 128 + D) {
+            const int ch = tid - 128;
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                w[q] = (uint32_t)(uint8_t)sV[(4 * q) * D + ch] |
+                       (uint32_t)(uint8_t)sV[(4 * q + 1) * D + ch] << 8 |
+                       (uint32_t)(uint8_t)sV[(4 * q + 2) * D + ch] << 16 |
+                       (uint32_t)(uint8_t)sV[(4 * q + 3) * D + ch] << 24;
+            *reinterpret_cast<i32x4 *>(vpage + kPage * ch) =
+                i32x4{(int32_t)w[0], (int32_t)w[1], (int32_t)w[2], (int32_t)w[3]};
         }
     } else {
         // A partial page (the first or last of the append): only its new slots
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append(AppendArgs a) {
         for (int o = tid; o < kPage * D; o += kAppendThreads) {
             const int ks = o / D, vs = o % kPage;
             if (ks >= s_lo && ks < s_hi) kpage[o] = sK[o];
-            if (vs >= s_lo && vs < s_hi) vpage[o] = sVT[o];
+            if (vs >= s_lo && vs < s_hi) vpage[o] = sV[vs * D + o / kPage];
         }
     }
 }
