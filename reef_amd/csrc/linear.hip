@@ -62,16 +62,16 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
     return c ^ ((r / rows256) & (kChunks - 1));
 }
 
-// One BM x BM output tile at (m0, n0) (BM = 128 or 64): 4 waves in a 2 x 2 grid,
-// each wave BM/2 x BM/2 in 32 x 32 blocks; the operand tiles of one stage are
-// BM x kBK (A) then BM x kBK (B) from the start of `smem`'s stage.
-template <int BM>
+// One BM x BN output tile at (m0, n0) (128 x 128, 128 x 64 or 64 x 64): 4 waves
+// in a 2 x 2 grid, each wave BM/2 x BN/2 in 32 x 32 blocks; the operand tiles of
+// one stage are BM x kBK (A) then BN x kBK (B) from the start of `smem`'s stage.
+template <int BM, int BN>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &a, int m0, int n0,
                                           int8_t (*smem)[kABytes + kBBytes]) {
-    constexpr int NBLK = BM / 64;                      // 32-wide blocks per wave and side
-    constexpr int TBYTES = BM * kBK;                   // one operand tile of a stage
-    constexpr int PA = TBYTES / 1024 / 4, PB = PA;     // 1 KB blocks per wave and operand
-    static_assert(PA >= 1 && 2 * TBYTES <= kABytes + kBBytes, "tile fits a stage");
+    constexpr int MI = BM / 64, NJ = BN / 64;          // 32-wide blocks per wave
+    constexpr int TA = BM * kBK, TB = BN * kBK;        // operand tiles of a stage
+    constexpr int PA = TA / 1024 / 4, PB = TB / 1024 / 4;  // 1 KB blocks per wave
+    static_assert(PA >= 1 && PB >= 1 && TA + TB <= kABytes + kBBytes, "tile fits a stage");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
@@ -102,7 +102,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, int m0, int n0,
     auto issue = [&](int s) {  // K step s (clamped to the last) into stage s % kStages
         const int k0 = min(s, steps - 1) * kBK;
         int8_t *sa = smem[s % kStages];
-        int8_t *sb = sa + TBYTES;
+        int8_t *sb = sa + TA;
         const bool in_k = k0 + kch < a.in;
 #pragma unroll
         for (int i = 0; i < PA; ++i)
@@ -116,18 +116,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, int m0, int n0,
                 in_k ? boff[i] : wbytes, k0, 0, 0);
     };
 
-    // Operand reads: row (BM/2) wm + 32 i + col (A) or (BM/2) wn + 32 j + col (B),
+    // Operand reads: row (BM/2) wm + 32 i + col (A) or (BN/2) wn + 32 j + col (B),
     // chunk 2 ks + grp; the swizzle depends on bits 2-3 of the row, i.e. of col.
     int rpos[kBK / 32];
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ++ks) rpos[ks] = 16 * chunk_pos(col, 2 * ks + grp);
-    const int arow = ((BM / 2) * wm + col) * kBK, brow = ((BM / 2) * wn + col) * kBK;
+    const int arow = ((BM / 2) * wm + col) * kBK, brow = ((BN / 2) * wn + col) * kBK;
 
-    i32x16 acc[NBLK][NBLK];
+    i32x16 acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < NBLK; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NBLK; ++j) acc[i][j] = i32x16{};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = i32x16{};
 
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s) issue(s);
@@ -145,37 +145,37 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, int m0, int n0,
         __builtin_amdgcn_s_barrier();
         issue(k + kStages - 1);
         const int8_t *sa = smem[k % kStages];
-        const int8_t *sb = sa + TBYTES;
+        const int8_t *sb = sa + TA;
 #pragma unroll
         for (int ks = 0; ks < kBK / 32; ++ks) {
-            i32x4 aop[NBLK], bop[NBLK];
+            i32x4 aop[MI], bop[NJ];
 #pragma unroll
-            for (int i = 0; i < NBLK; ++i)
+            for (int i = 0; i < MI; ++i)
                 aop[i] = *reinterpret_cast<const i32x4 *>(sa + arow + 32 * i * kBK + rpos[ks]);
 #pragma unroll
-            for (int j = 0; j < NBLK; ++j)
+            for (int j = 0; j < NJ; ++j)
                 bop[j] = *reinterpret_cast<const i32x4 *>(sb + brow + 32 * j * kBK + rpos[ks]);
 #pragma unroll
-            for (int i = 0; i < NBLK; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < NBLK; ++j) acc[i][j] = mfma_32x32x32_i8(aop[i], bop[j], acc[i][j]);
+                for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_32x32x32_i8(aop[i], bop[j], acc[i][j]);
         }
     }
     // The trailing loads of the clamped last steps must land before the workgroup's
     // LDS can be handed to another workgroup.
     __builtin_amdgcn_s_waitcnt(0xf70);
 
-    // Epilogue: lane holds output column n0 + (BM/2) wn + 32 j + col and, in
+    // Epilogue: lane holds output column n0 + (BN/2) wn + 32 j + col and, in
     // register 4 q + e, row m0 + (BM/2) wm + 32 i + 8 q + 4 grp + e.
     bool bad = false;
 #pragma unroll
-    for (int j = 0; j < NBLK; ++j) {
-        const int n = n0 + (BM / 2) * wn + 32 * j + col;
+    for (int j = 0; j < NJ; ++j) {
+        const int n = n0 + (BN / 2) * wn + 32 * j + col;
         if (n >= a.out) continue;
         const float wsc = a.ws[n];
         const float bn = a.bias ? a.bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < NBLK; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (r >> 2) + 4 * grp + (r & 3);
@@ -195,12 +195,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, int m0, int n0,
 }
 
 // Workgroups [0, n_big) take the 128 x 128 tiles [0, n_big) in tile order (tiles
-// along `out` fastest); when there are a few more tiles than compute units, the
-// remaining tiles are cut into four 64 x 64 quadrants, one workgroup each, so that
-// every compute unit holds one large tile and at most one quadrant instead of some
-// holding two large tiles while the others idle. Workgroup i runs on XCD
-// i % 8: each XCD gets a contiguous run of the large tiles and of the quadrants.
-__global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a, int n_big) {
+// along `out` fastest). When there are a few more tiles than compute units, the
+// remaining tiles are cut into `pieces` (4: 64 x 64 quadrants, 2: 128 x 64 halves),
+// one workgroup each, so that every compute unit holds one large tile and at most
+// one piece instead of some holding two large tiles while the others idle.
+// Workgroup i runs on XCD i % 8: each XCD gets a contiguous run of the large
+// tiles and of the pieces.
+__global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a, int n_big,
+                                                                    int pieces) {
     static_assert(kBN == kBM, "square tiles");
     __shared__ __attribute__((aligned(16))) int8_t smem[kStages][kABytes + kBBytes];  // [stage] A, B
     const int g = (int)blockIdx.x;
@@ -210,12 +212,16 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_w8a8_kernel(GemmArgs a, 
     };
     if (g < n_big) {
         const int t = xcd_rank(g, n_big);
-        gemm_tile<kBM>(a, t / a.n_tiles * kBM, t % a.n_tiles * kBM, smem);
-    } else {
+        gemm_tile<kBM, kBN>(a, t / a.n_tiles * kBM, t % a.n_tiles * kBN, smem);
+    } else if (pieces == 4) {
         const int s = xcd_rank(g - n_big, (int)gridDim.x - n_big);
         const int t = n_big + s / 4, q = s % 4;
-        gemm_tile<kBM / 2>(a, t / a.n_tiles * kBM + (kBM / 2) * (q >> 1),
-                           t % a.n_tiles * kBM + (kBM / 2) * (q & 1), smem);
+        gemm_tile<kBM / 2, kBN / 2>(a, t / a.n_tiles * kBM + (kBM / 2) * (q >> 1),
+                                    t % a.n_tiles * kBN + (kBN / 2) * (q & 1), smem);
+    } else {
+        const int s = xcd_rank(g - n_big, (int)gridDim.x - n_big);
+        const int t = n_big + s / 2, q = s % 2;
+        gemm_tile<kBM, kBN / 2>(a, t / a.n_tiles * kBM, t % a.n_tiles * kBN + (kBN / 2) * q, smem);
     }
 }
 
@@ -237,18 +243,23 @@ reef_status launch_gemm(const int8_t *xq, const float *xs, int64_t rows, int64_t
     a.m_tiles = (int32_t)ceil_div(rows, kBM);
     a.status = status;
     const int64_t tiles = (int64_t)a.m_tiles * a.n_tiles;
-    // Up to a quarter more tiles than compute units: the tiles past one per unit go
-    // as quadrants, so the grid is at most two workgroups per unit (measured on
-    // 4096 x 8192 -> 1280, 320 tiles: 64.5 us against 70.4; with more tiles the
-    // extra quadrants queue and it loses: 384 tiles 84.9 against 80.7 us).
-    // REEF_GEMM_QUADRANTS=0 turns this off.
+    // A few more tiles than compute units: the tiles past one per unit go as
+    // pieces, so the grid is at most two workgroups per unit: quadrants for up to a
+    // quarter more tiles, halves for up to half more. (Measured on 4096 x 8192 ->
+    // 1280, 320 tiles: 64.5 us against 70.4 with quadrants; cut into quadrants, 384
+    // tiles queue and lose: 84.9 against 80.7 us.) REEF_GEMM_QUADRANTS=0 turns the
+    // pieces off.
     const int64_t cus = compute_units();
     const char *env = getenv("REEF_GEMM_QUADRANTS");
-    const bool quads = (env ? atoi(env) != 0 : true) && tiles > cus && 4 * (tiles - cus) <= cus;
-    const int64_t n_big = quads ? cus : tiles;
-    const int64_t grid = n_big + 4 * (tiles - n_big);
+    const int64_t extra = tiles - cus;
+    const int pieces = !(env ? atoi(env) != 0 : true) || extra <= 0 ? 1
+                       : 4 * extra <= cus                        ? 4
+                       : 2 * extra <= cus                        ? 2
+                                                                 : 1;
+    const int64_t n_big = pieces > 1 ? cus : tiles;
+    const int64_t grid = n_big + pieces * (tiles - n_big);
     hipLaunchKernelGGL(gemm_w8a8_kernel, dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, a,
-                       (int)n_big);
+                       (int)n_big, pieces);
     return launch_status();
 }
 

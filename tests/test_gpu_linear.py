@@ -100,16 +100,18 @@ def test_linear_errors(reef):
     assert np.all(np.isfinite(y))
 
 
+@pytest.mark.parametrize("rows,fout", [(2000, 2500), (2000, 2980)])
 @pytest.mark.parametrize("quadrants", ["1", "0"])
-def test_linear_quadrant_tiles(reef, quadrants, monkeypatch):
-    """2000 x 256 -> 2500: 16 x 20 = 320 output tiles of 128 x 128, between one and
-    two per compute unit, so the tiles past the first 256 run as four 64 x 64
-    quadrants each (including the ragged last row and column of tiles). Bit-exact
-    against the oracle with the quadrants and with whole tiles only."""
+def test_linear_quadrant_tiles(reef, rows, fout, quadrants, monkeypatch):
+    """2000 x 256 -> 2500: 16 x 20 = 320 output tiles of 128 x 128, a quarter more
+    than the 256 compute units, so the tiles past the first 256 run as four 64 x 64
+    quadrants each; -> 2980: 16 x 24 = 384 tiles, cut into two 128 x 64 halves. The
+    pieces include the ragged last row and column of tiles. Bit-exact against the
+    oracle with the pieces and with whole tiles only."""
     monkeypatch.setenv("REEF_GEMM_QUADRANTS", quadrants)
-    rows, fin, fout = 2000, 256, 2500
-    case(f"w8a8 rows{rows} in{fin} out{fout} quadrants={quadrants}")
-    rng = np.random.default_rng(77)
+    fin = 256
+    case(f"w8a8 rows{rows} in{fin} out{fout} pieces={quadrants}")
+    rng = np.random.default_rng(77 + fout)
     x = rng.standard_normal((rows, fin)).astype(np.float32)
     w = rng.integers(-127, 128, (fout, fin), dtype=np.int8)
     ws = rng.uniform(0.001, 0.02, fout).astype(np.float32)
