@@ -45,10 +45,13 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate budget of the CPU-baseline sample")
-    ap.add_argument("--prefill", default="c2", choices=["c1", "c2", "c4", "c5a"],
-                    help="prefill workload to time (c2, the headline, by default)")
-    ap.add_argument("--decode", default="c3,c5b",
-                    help="decode workloads to time (comma list of c3, c5b)")
+    ap.add_argument("--prefill", default="prefill_1x32x2048x128",
+                    choices=["prefill_1x1x128x64", "prefill_1x32x2048x128",
+                             "prefill_4x32x8192x128", "prefill_1x8x4096x128_gqa"],
+                    help="prefill workload to time (the headline 1x32x2048x128 by default)")
+    ap.add_argument("--decode", default="decode_b64_l4096,decode_paged_b128_ragged",
+                    help="decode workloads to time (comma list of decode_b64_l4096, "
+                         "decode_paged_b128_ragged)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the W8A8 projection, integer-only head and KV-append lines")
     ap.add_argument("--profile-pass", action="store_true",
@@ -191,8 +194,8 @@ def bench_prefill(torch, reef, W, args):
     return cfg, ops, wall_ms, kern_ms, (quant_ms, quant_how), quant_bytes, (q, k, v, qs, ks, vs)
 
 
-def decode_c3(torch, reef, W, steps, warmup, num_splits=0):
-    cfg = W.CONFIGS["c3"]
+def decode_contiguous(torch, reef, W, steps, warmup, num_splits=0):
+    cfg = W.CONFIGS["decode_b64_l4096"]
     g = torch.Generator(device="cuda")
     g.manual_seed(cfg.seed)
     B, Hq, Hkv, D, L = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.context
@@ -219,10 +222,10 @@ def decode_c3(torch, reef, W, steps, warmup, num_splits=0):
     return cfg, cfg.kv_bytes(), wall_ms, kern_ms
 
 
-def decode_c5b(torch, reef, W, steps, warmup, pools=3, num_splits=0):
+def decode_paged_ragged(torch, reef, W, steps, warmup, pools=3, num_splits=0):
     """Ragged paged decode. The pages of one step (about 150 MB) fit in the 256 MB
     last-level cache, so steps rotate over `pools` independent page pools."""
-    cfg = W.CONFIGS["c5b"]
+    cfg = W.CONFIGS["decode_paged_b128_ragged"]
     B, Hq, Hkv, D = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim
     lens = cfg.lengths()
     npages = (lens + 15) // 16
@@ -312,7 +315,7 @@ def bench_extras(torch, reef, W, steps):
                           "frac_int8_peak": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
     del x, w, y, wsp, xq
     # integer-only head, 1x32x2048x128 causal
-    cfg = W.CONFIGS["c2"]
+    cfg = W.CONFIGS["prefill_1x32x2048x128"]
     qi = torch.randint(-127, 128, (1, 32, 2048, 128), dtype=torch.int8, device="cuda", generator=g)
     ki = torch.randint(-127, 128, (1, 32, 2048, 128), dtype=torch.int8, device="cuda", generator=g)
     vi = torch.randint(-127, 128, (1, 32, 2048, 128), dtype=torch.int8, device="cuda", generator=g)
@@ -377,7 +380,7 @@ def copy_calibration(torch):
 def recorded_traffic(workload):
     """HBM bytes per prefill launch measured by the hardware counters and recorded
     in profiles/ (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration)."""
-    path = os.path.join(ROOT, "profiles", f"prefill_{workload}_hbm_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"{workload}_hbm_traffic.md")
     try:
         with open(path) as f:
             text = f.read()
@@ -440,7 +443,7 @@ def main():
         copy_calibration(torch)
         args.steps, args.warmup = 3, 1
         bench_prefill(torch, reef, W, args)
-        fns = {"c3": decode_c3, "c5b": decode_c5b}
+        fns = {"decode_b64_l4096": decode_contiguous, "decode_paged_b128_ragged": decode_paged_ragged}
         for fn in (fns[n] for n in args.decode.split(",") if n):
             fn(torch, reef, W, 3, 1)
         if not args.no_extra:
@@ -482,7 +485,7 @@ def main():
     }
     if not args.no_decode:
         dec = []
-        fns = {"c3": decode_c3, "c5b": decode_c5b}
+        fns = {"decode_b64_l4096": decode_contiguous, "decode_paged_b128_ragged": decode_paged_ragged}
         for fn in (fns[n] for n in args.decode.split(",") if n):
             dcfg, nbytes, dwall, dkern = fn(torch, reef, W, max(10, args.steps // 2), 5)
             gbs = nbytes / (dkern * 1e-3) / 1e9

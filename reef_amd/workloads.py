@@ -122,16 +122,16 @@ class DecodeConfig:
 
 
 CONFIGS = {
-    "c1": PrefillConfig("causal prefill 1x1x128x64, per-tensor", 1, 1, 1, 128, 64, 0, seed=1),
-    "c2": PrefillConfig("causal prefill 1x32x2048x128, per-head", 1, 32, 32, 2048, 128, 1,
+    "prefill_1x1x128x64": PrefillConfig("causal prefill 1x1x128x64, per-tensor", 1, 1, 1, 128, 64, 0, seed=1),
+    "prefill_1x32x2048x128": PrefillConfig("causal prefill 1x32x2048x128, per-head", 1, 32, 32, 2048, 128, 1,
                         seed=2),
-    "c3": DecodeConfig("decode B64 32q/8kv L4096 d128, per-token KV", 64, 32, 8, 128, 4096,
+    "decode_b64_l4096": DecodeConfig("decode B64 32q/8kv L4096 d128, per-token KV", 64, 32, 8, 128, 4096,
                        seed=3),
-    "c4": PrefillConfig("causal prefill 4x32x8192x128, per-head, 1% x8 outliers", 4, 32, 32,
+    "prefill_4x32x8192x128": PrefillConfig("causal prefill 4x32x8192x128, per-head, 1% x8 outliers", 4, 32, 32,
                         8192, 128, 1, seed=4, outlier_fraction=0.01),
-    "c5a": PrefillConfig("causal prefill 1x8q/1kv x4096x128, per-head", 1, 8, 1, 4096, 128, 1,
+    "prefill_1x8x4096x128_gqa": PrefillConfig("causal prefill 1x8q/1kv x4096x128, per-head", 1, 8, 1, 4096, 128, 1,
                          seed=5),
-    "c5b": DecodeConfig("ragged paged decode B128 8q/1kv L~U[512,8192] d128, page 16", 128, 8,
+    "decode_paged_b128_ragged": DecodeConfig("ragged paged decode B128 8q/1kv L~U[512,8192] d128, page 16", 128, 8,
                         1, 128, 8192, min_context=512, paged=True, seed=6),
 }
 

@@ -200,7 +200,7 @@ def _run_prefill(reef, q, k, v, p, precise=False, workspace=None):
 
 
 def test_prefill_config1(reef):
-    cfg = W.CONFIGS["c1"]
+    cfg = W.CONFIGS["prefill_1x1x128x64"]
     case(f"prefill {cfg.name}")
     q, k, v = W.host_prefill_inputs(cfg)
     # the kernels' quantization is bit-identical to the oracle's
