@@ -95,3 +95,32 @@ def test_integer_head_long_sequence(reef):
                                            score_shift=10, out_shift=8))
     gold = oracle.attend_head_int8(q[0, 0], k[0, 0], v[0, 0], 0, 0, 10, 8)
     assert np.array_equal(out[0, 0], gold)
+
+
+def test_integer_head_random_shapes(reef):
+    """Twelve seeded shapes: query offsets, windows that start mid-tile, GQA, head
+    dims 32/64/128, lengths that are not multiples of the 64-key tile (staged K and
+    V tiles partly past kv_len, waves with no rows). Bit-exact against the oracle."""
+    rng = np.random.default_rng(2024)
+    for i in range(12):
+        D = int(rng.choice([32, 64, 128]))
+        Hkv = int(rng.integers(1, 3))
+        Hq = Hkv * int(rng.choice([1, 2, 4]))
+        Sq = int(rng.integers(1, 300))
+        Skv = Sq + int(rng.integers(0, 200))
+        start = Skv - Sq if rng.random() < 0.5 else int(rng.integers(0, Skv - Sq + 1))
+        window = 0 if rng.random() < 0.5 else int(rng.integers(1, 150))
+        shift = int(rng.integers(6, 12))
+        case(f"integer head random {i}: Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} start{start} "
+             f"win{window} shift{shift}")
+        q = rng.integers(-127, 128, (1, Hq, Sq, D), dtype=np.int8)
+        k = rng.integers(-127, 128, (1, Hkv, Skv, D), dtype=np.int8)
+        v = rng.integers(-127, 128, (1, Hkv, Skv, D), dtype=np.int8)
+        out = host(reef.attention_int8_integer(gpu(q), gpu(k), gpu(v), table_gpu(),
+                                               score_shift=shift, out_shift=8,
+                                               query_start=start, window=window))
+        group = Hq // Hkv
+        for h in range(Hq):
+            gold = oracle.attend_head_int8(q[0, h], k[0, h // group], v[0, h // group], start,
+                                           window, shift, 8)
+            assert np.array_equal(out[0, h], gold), (i, h)
