@@ -172,20 +172,29 @@ def quant_graph_ms(torch, launch, steps=20, warmup=3):
     return timed(torch, g.replay, steps, warmup)[1], "one HIP graph of the launches"
 
 
-def bench_prefill(torch, reef, W, args):
-    cfg = W.CONFIGS[args.prefill]
+def prefill_setup(torch, reef, W, name):
+    """The inputs of prefill workload `name` drawn on the GPU and quantized by the
+    library, the fp32 output buffer, and the launch the bench times (the tests of the
+    benchmark workloads call this same launch)."""
+    cfg = W.CONFIGS[name]
     qf, kf, vf = W.device_prefill_inputs(cfg)
     quantize = reef.quantize_per_head if cfg.granularity == 1 else reef.quantize_per_tensor
     q, qs = quantize(qf)
     k, ks = quantize(kf)
     v, vs = quantize(vf)
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    launch = prefill_launcher(torch, reef, cfg, q, k, v, qs, ks, vs, out)
+    return cfg, (qf, kf, vf), (q, k, v, qs, ks, vs), out, launch
+
+
+def bench_prefill(torch, reef, W, args):
+    cfg, (qf, kf, vf), (q, k, v, qs, ks, vs), out, launch = prefill_setup(
+        torch, reef, W, args.prefill)
 
     quant = quant_launcher(torch, reef, cfg, (qf, kf, vf))
     quant_ms, quant_how = quant_graph_ms(torch, quant)
     quant.check()
-    del qf, kf, vf
-    launch = prefill_launcher(torch, reef, cfg, q, k, v, qs, ks, vs, out)
+    del qf, kf, vf, quant
     wall_ms, kern_ms = timed(torch, launch, args.steps, args.warmup)
     if not torch.isfinite(out).all():
         raise RuntimeError("prefill produced non-finite output")
@@ -194,13 +203,24 @@ def bench_prefill(torch, reef, W, args):
     return cfg, ops, wall_ms, kern_ms, (quant_ms, quant_how), quant_bytes, (q, k, v, qs, ks, vs)
 
 
-def decode_contiguous(torch, reef, W, steps, warmup, num_splits=0):
+def decode_query(torch, reef, cfg, g):
+    """The one-token queries [B, Hq, D] of a decode workload, N(0, 1), quantized with
+    one scale per query head over the batch (PER_HEAD)."""
+    B, Hq, D = cfg.batch, cfg.q_heads, cfg.head_dim
+    qf = torch.randn((B, Hq, 1, D), generator=g, device="cuda")
+    q, qsc = reef.quantize_per_head(qf)
+    return q.view(B, Hq, D), qsc
+
+
+def decode_contiguous_setup(torch, reef, W, num_splits=0):
+    """The B64 32q/8kv L4096 decode workload on the GPU and the launch the bench
+    times: returns (cfg, launch, tensors) with tensors = (q, q_scales, k, v_pages,
+    k_scales, v_scales, out)."""
     cfg = W.CONFIGS["decode_b64_l4096"]
     g = torch.Generator(device="cuda")
     g.manual_seed(cfg.seed)
     B, Hq, Hkv, D, L = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.context
-    qf = torch.randn((B, Hq, D), generator=g, device="cuda")
-    q, qsc = reef.quantize_rows(qf)
+    q, qsc = decode_query(torch, reef, cfg, g)
     kf = torch.randn((B, Hkv, L, D), generator=g, device="cuda")
     k, ksc = reef.quantize_rows(kf)
     del kf
@@ -211,20 +231,30 @@ def decode_contiguous(torch, reef, W, steps, warmup, num_splits=0):
     del vq
     out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
     status = reef.StatusWord()
-    p = reef._decode_params(q, L, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN, num_splits)
+    p = reef._decode_params(q, L, Hkv, 0, 1 / math.sqrt(D), reef.PER_HEAD, num_splits)
     ws = reef.decode_workspace(p, q.device)
 
     def launch():
         reef.attention_decode(q, qsc, k, vp, ksc, vsc, None, softmax_scale=1 / math.sqrt(D),
-                              num_splits=num_splits, workspace=ws, status=status, out=out)
+                              q_granularity=reef.PER_HEAD, num_splits=num_splits, workspace=ws,
+                              status=status, out=out)
+    launch.check = lambda: status.check("decode")
+    return cfg, launch, (q, qsc, k, vp, ksc, vsc, out)
+
+
+def decode_contiguous(torch, reef, W, steps, warmup, num_splits=0):
+    cfg, launch, _ = decode_contiguous_setup(torch, reef, W, num_splits)
     wall_ms, kern_ms = timed(torch, launch, steps, warmup)
-    status.check("decode")
+    launch.check()
     return cfg, cfg.kv_bytes(), wall_ms, kern_ms
 
 
-def decode_paged_ragged(torch, reef, W, steps, warmup, pools=3, num_splits=0):
-    """Ragged paged decode. The pages of one step (about 150 MB) fit in the 256 MB
-    last-level cache, so steps rotate over `pools` independent page pools."""
+def decode_paged_setup(torch, reef, W, pools=3, num_splits=0):
+    """The ragged paged B128 8q/1kv decode workload. The pages of one step (about
+    150 MB) fit in the 256 MB last-level cache, so successive launches rotate over
+    `pools` independent page pools. Returns (cfg, lens, launch, setups, (q,
+    q_scales, out)); setups[i] = (k_pages, v_pages, k_scale_pages, v_scale_pages,
+    block_table) of pool i, and launch(i) runs on pool i (launch() on the next)."""
     cfg = W.CONFIGS["decode_paged_b128_ragged"]
     B, Hq, Hkv, D = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim
     lens = cfg.lengths()
@@ -234,8 +264,7 @@ def decode_paged_ragged(torch, reef, W, steps, warmup, pools=3, num_splits=0):
     max_blocks = cfg.context // 16
     g = torch.Generator(device="cuda")
     g.manual_seed(cfg.seed)
-    qf = torch.randn((B, Hq, D), generator=g, device="cuda")
-    q, qsc = reef.quantize_rows(qf)
+    q, qsc = decode_query(torch, reef, cfg, g)
     setups = []
     for i in range(pools):
         kf = torch.randn((pool_pages, Hkv, 16, D), generator=g, device="cuda")
@@ -256,19 +285,27 @@ def decode_paged_ragged(torch, reef, W, steps, warmup, pools=3, num_splits=0):
     lens_t = torch.from_numpy(lens.astype(np.int32)).cuda()
     out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
     status = reef.StatusWord()
-    p = reef._decode_params(q, max_blocks * 16, Hkv, 0, 1 / math.sqrt(D), reef.PER_TOKEN,
+    p = reef._decode_params(q, max_blocks * 16, Hkv, 0, 1 / math.sqrt(D), reef.PER_HEAD,
                             num_splits)
     ws = reef.decode_workspace(p, q.device)
     it = [0]
 
-    def launch():
-        kp, vp, ksp, vsp, table = setups[it[0] % pools]
-        it[0] += 1
+    def launch(pool=None):
+        if pool is None:
+            pool = it[0] % pools
+            it[0] += 1
+        kp, vp, ksp, vsp, table = setups[pool]
         reef.attention_decode_paged(q, qsc, kp, vp, ksp, vsp, table, lens_t,
-                                    softmax_scale=1 / math.sqrt(D), num_splits=num_splits,
-                                    workspace=ws, status=status, out=out)
+                                    softmax_scale=1 / math.sqrt(D), q_granularity=reef.PER_HEAD,
+                                    num_splits=num_splits, workspace=ws, status=status, out=out)
+    launch.check = lambda: status.check("decode paged")
+    return cfg, lens, launch, setups, (q, qsc, out)
+
+
+def decode_paged_ragged(torch, reef, W, steps, warmup, pools=3, num_splits=0):
+    cfg, lens, launch, _, _ = decode_paged_setup(torch, reef, W, pools, num_splits)
     wall_ms, kern_ms = timed(torch, launch, steps, warmup)
-    status.check("decode paged")
+    launch.check()
     return cfg, cfg.kv_bytes(lens), wall_ms, kern_ms
 
 

@@ -143,6 +143,22 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
 /* Attention flags. */
 #define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts (always on
                                      * with PER_TOKEN K/V scales) */
+/* Prefill work schedule (bits 4-6 of flags). AUTO lets the library choose from the
+ * grid size and the workspace; the others force one schedule, for callers that
+ * tune it and for tests that must reach every path. A forced schedule that the
+ * call cannot use (BALANCED without a large enough workspace, or with PRECISE_PV or
+ * PER_TOKEN K/V scales) returns REEF_INVALID_ARGUMENT. */
+#define REEF_ATTN_SCHED_MASK 0x70u
+#define REEF_ATTN_SCHED_AUTO 0x00u
+#define REEF_ATTN_SCHED_ONE_ITEM 0x10u /* one 128-row query tile per workgroup */
+#define REEF_ATTN_SCHED_SPLIT 0x20u    /* persistent workgroups; two 4-wave groups split
+                                        * each tile's keys */
+#define REEF_ATTN_SCHED_BALANCED 0x30u /* equal (tile, key block) ranges per workgroup;
+                                        * cut tiles merge through the workspace */
+#define REEF_ATTN_SCHED_PACKED 0x40u   /* head_dim 128, per-tensor / per-head K and V
+                                        * scales: V packed once into an fp16 image in the
+                                        * workspace, 256-row query tiles, persistent
+                                        * workgroups over (light, heavy) tile pairs */
 
 typedef struct reef_attention_params {
     int64_t batch, q_heads, kv_heads; /* q head h reads kv head h / (q_heads / kv_heads) */
@@ -163,10 +179,12 @@ typedef struct reef_attention_params {
  * throws for a row with none, activation.hpp:204-207).
  *
  * workspace (optional, 256-byte aligned, at least
- * reef_attention_prefill_workspace_bytes(p) bytes; NULL/0 allowed) lets grids
- * with few query tiles per compute unit split the causal work evenly over the
- * GPU: it must be zero-filled before its first use, and every call leaves it
- * zero-filled. Calls that may run at the same time need separate workspaces. */
+ * reef_attention_prefill_workspace_bytes(p) bytes; NULL/0 allowed) holds the
+ * counters and partial results of the balanced schedule and, for head_dim 128, the
+ * fp16 value image of the packed schedule (2 bytes per V element). It must be
+ * zero-filled before its first use; every call leaves the counters zero-filled.
+ * Without it the library uses the schedules that need none. Calls that may run at
+ * the same time need separate workspaces. */
 size_t reef_attention_prefill_workspace_bytes(const reef_attention_params *p);
 
 reef_status reef_attention_prefill_int8(const reef_attention_params *p, const int8_t *q,

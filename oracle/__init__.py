@@ -63,6 +63,7 @@ def _load() -> C.CDLL:
         "ro_quantize_rows": (C.c_int, [_f32p, _sz, _sz, _i8p, _f32p]),
         "ro_quantize_per_tensor": (C.c_int, [_f32p, _sz, _i8p, _f32p]),
         "ro_quantize_per_head": (C.c_int, [_f32p, _sz, _sz, _sz, _sz, _i8p, _f32p]),
+        "ro_dequantize": (None, [_i8p, _sz, _sz, _f32p, _f32p]),
         "ro_exp_nonpositive": (C.c_float, [C.c_float]),
         "ro_visible": (C.c_int, [_i64, _i64, _i64, _i64]),
         "ro_qk_i32": (None, [_i8p, _i8p, _sz, _sz, _sz, _i32p]),
@@ -150,6 +151,18 @@ def quantize_per_token(x):
     x = _c(x, np.float32)
     q, s = quantize_rows(x.reshape(-1, x.shape[-1]))
     return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+def dequantize(q, scales, group: int):
+    """float(q[i]) * scales[i // group] for a flat int8 array (the engine's
+    static_cast<float>(code) * scale, tests/test_int8.cpp:182)."""
+    q = _c(q, np.int8).reshape(-1)
+    scales = _c(scales, np.float32).reshape(-1)
+    if group <= 0 or len(scales) < (q.size + group - 1) // group:
+        raise ValueError("dequantize: group and scales do not cover the values")
+    x = np.empty(q.size, np.float32)
+    lib().ro_dequantize(q, q.size, group, scales, x)
+    return x
 
 
 # --- math / softmax / heads ---------------------------------------------------------

@@ -108,6 +108,17 @@ int ro_quantize_per_head(const float *x, size_t B, size_t H, size_t S, size_t D,
     return status;
 }
 
+/* The engine's dequantization of an int8 code, static_cast<float>(code) * scale
+ * (tests/test_int8.cpp:182; quant.hpp:34: "row r of the real weight is
+ * approximately values row r times scales[r]"): one correctly rounded product.
+ * Value i uses scales[i / group] (group = row width for per-row scales, n for one
+ * scale over the tensor). */
+void ro_dequantize(const int8_t *q, size_t n, size_t group, const float *scales, float *x) {
+    for (size_t i = 0; i < n; ++i) {
+        x[i] = (float)q[i] * scales[i / group];
+    }
+}
+
 /* math.hpp:34-67: x = k ln2 + r, Cephes expf polynomial for e^r, times 2^k.
  * Every step is one correctly rounded float operation, in the engine's
  * order; 2^k is assembled from its exponent field. */

@@ -45,6 +45,9 @@ int ro_quantize_per_tensor(const float *x, size_t n, int8_t *q, float *scale);
 int ro_quantize_per_head(const float *x, size_t B, size_t H, size_t S, size_t D, int8_t *q,
                          float *scales);
 
+/* static_cast<float>(code) * scale (tests/test_int8.cpp:182), scales[i / group]. */
+void ro_dequantize(const int8_t *q, size_t n, size_t group, const float *scales, float *x);
+
 /* math.hpp:34-67 (Cephes expf polynomial, for x <= 0). */
 float ro_exp_nonpositive(float x);
 

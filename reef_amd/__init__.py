@@ -24,6 +24,9 @@ LIB_PATH = os.path.join(PKG, "libreef_hip.so")
 OK, INVALID_ARGUMENT, NON_FINITE_INPUT, CAPACITY, HIP_ERROR, UNSUPPORTED, OVERFLOW = range(7)
 PER_TENSOR, PER_HEAD, PER_TOKEN = 0, 1, 2
 ATTN_PRECISE_PV = 0x1
+# prefill schedules (reef_attention_params.flags bits 4-6)
+SCHED_AUTO, SCHED_ONE_ITEM, SCHED_SPLIT, SCHED_BALANCED, SCHED_PACKED = (0x00, 0x10, 0x20,
+                                                                         0x30, 0x40)
 PAGE = 16
 
 EXPORTS = [
@@ -286,15 +289,15 @@ def prefill_workspace(params: AttentionParams, device):
 
 def attention_prefill(q, k, v, q_scales, k_scales, v_scales, *, query_start=None, window=0,
                       softmax_scale=None, q_granularity=PER_HEAD, kv_granularity=PER_HEAD,
-                      precise=False, out=None, workspace=None):
+                      precise=False, schedule=SCHED_AUTO, out=None, workspace=None):
     """Attention::context (attention.hpp:374-432) over int8 heads in one launch.
 
     q [B, Hq, Sq, D], k and v [B, Hkv, Skv, D] int8 (contiguous head_dim, any other
     strides); scales by granularity. softmax_scale defaults to 1/sqrt(D); pass 1.0
-    for the engine's unscaled scores. Returns fp32 [B, Hq, Sq, D]. workspace: None
-    takes this stream's cached one (prefill_workspace), False passes none (grids
-    with few query tiles then take the unbalanced kernels), or a zero-filled uint8
-    tensor of reef_attention_prefill_workspace_bytes bytes.
+    for the engine's unscaled scores. Returns fp32 [B, Hq, Sq, D]. schedule is one
+    of the SCHED_* flags (SCHED_AUTO: the library's choice). workspace: None takes
+    this stream's cached one (prefill_workspace), False passes none, or a
+    zero-filled uint8 tensor of reef_attention_prefill_workspace_bytes bytes.
     """
     torch = _torch()
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
@@ -309,7 +312,7 @@ def attention_prefill(q, k, v, q_scales, k_scales, v_scales, *, query_start=None
         softmax_scale = 1.0 / math.sqrt(D)
     start = Skv - Sq if query_start is None else query_start
     p = AttentionParams(B, Hq, Hkv, Sq, Skv, D, start, window, softmax_scale, q_granularity,
-                        kv_granularity, ATTN_PRECISE_PV if precise else 0)
+                        kv_granularity, (ATTN_PRECISE_PV if precise else 0) | schedule)
     if out is None:
         out = torch.empty((B, Hq, Sq, D), dtype=torch.float32, device=q.device)
     qs, ks, vs, os_ = _strides4(q), _strides4(k), _strides4(v), _strides4(out)

@@ -426,8 +426,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
     }
 
     // With more than one workgroup per (sequence, kv head), every part writes
-    // (max, sum, output) to its workspace slot with device-coherent stores, waits
-    // for them and counts itself in on the item's counter; the last part merges
+    // (max, sum, output) to its workspace slot with device-coherent atomic stores,
+    // releases them at agent scope and counts itself in on the item's counter (an
+    // acquire-release increment); the last part acquires at agent scope, merges
     // the slots in part order (its own from registers, explicit fused
     // multiply-adds: the same result whichever part finishes last), stores the
     // output and resets the counter. No second kernel combines splits.
@@ -451,13 +452,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs
         }
         __hip_atomic_store(so + DecodeSlot<D>::O * kWave + lane, pack(m, l), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);  // the slot is complete before the count
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the slot before the count
         uint32_t ticket = 0;
         if (lane == 0)
-            ticket = __hip_atomic_fetch_add(a.counters + item, 1u, __ATOMIC_RELAXED,
+            ticket = __hip_atomic_fetch_add(a.counters + item, 1u, __ATOMIC_ACQ_REL,
                                             __HIP_MEMORY_SCOPE_AGENT);
         ticket = __shfl(ticket, 0);
         if (ticket != (uint32_t)(parts - 1)) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other parts' slots
         if (lane == 0)
             __hip_atomic_store(a.counters + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         auto get = [](const uint64_t *q) {

@@ -34,7 +34,6 @@ constexpr int kXcds = 8;
 #define REEF_GEMM_STAGES 2
 #endif
 constexpr int kBM = 128, kBN = REEF_GEMM_BN;  // output tile: rows x out features
-constexpr int kNB = kBN / 64;                 // 32-wide column blocks per wave
 constexpr int kBK = REEF_GEMM_BK;             // bytes of K per step
 constexpr int kStages = REEF_GEMM_STAGES;
 constexpr int kABytes = kBM * kBK, kBBytes = kBN * kBK;  // operand tiles of one stage
@@ -247,15 +246,13 @@ reef_status launch_gemm(const int8_t *xq, const float *xs, int64_t rows, int64_t
     // pieces, so the grid is at most two workgroups per unit: quadrants for up to a
     // quarter more tiles, halves for up to half more. (Measured on 4096 x 8192 ->
     // 1280, 320 tiles: 64.5 us against 70.4 with quadrants; cut into quadrants, 384
-    // tiles queue and lose: 84.9 against 80.7 us.) REEF_GEMM_QUADRANTS=0 turns the
-    // pieces off.
+    // tiles queue and lose: 84.9 against 80.7 us.)
     const int64_t cus = compute_units();
-    const char *env = getenv("REEF_GEMM_QUADRANTS");
     const int64_t extra = tiles - cus;
-    const int pieces = !(env ? atoi(env) != 0 : true) || extra <= 0 ? 1
-                       : 4 * extra <= cus                        ? 4
-                       : 2 * extra <= cus                        ? 2
-                                                                 : 1;
+    const int pieces = extra <= 0         ? 1
+                       : 4 * extra <= cus ? 4
+                       : 2 * extra <= cus ? 2
+                                          : 1;
     const int64_t n_big = pieces > 1 ? cus : tiles;
     const int64_t grid = n_big + pieces * (tiles - n_big);
     hipLaunchKernelGGL(gemm_w8a8_kernel, dim3((unsigned)grid), dim3(kGemmThreads), 0, stream, a,

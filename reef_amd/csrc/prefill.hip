@@ -27,6 +27,16 @@
 #include "reef_common.hpp"
 
 namespace reef {
+
+// The packed schedule (prefill_packed.hip).
+int64_t packed_image_bytes(int64_t batch, int64_t kv_heads, int64_t kv_len);
+reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *q,
+                                  const int64_t (&qst)[3], const int8_t *k,
+                                  const int64_t (&kst)[3], const int8_t *v,
+                                  const int64_t (&vst)[3], const float *q_scales,
+                                  const float *k_scales, const float *v_scales, float *out,
+                                  const int64_t (&ost)[3], void *image, hipStream_t stream);
+
 namespace {
 
 constexpr int kBM = 128;  // query rows per workgroup
@@ -45,6 +55,9 @@ struct PrefillArgs {
     int32_t q_gran, kv_gran;
     int32_t q_tiles;
     int32_t zigzag;  // pair heavy and light tiles in grids that fit at once
+    // Items this launch computes (per-tensor / per-head K/V scales): 0 all, 1 those
+    // whose largest dequantized value 127 s_v is at most kPreciseAbove, 2 the others.
+    int32_t item_sel;
 };
 
 // Balanced schedule: the steps (item, key tile) of all items, items in (batch,
@@ -288,9 +301,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     // groups vary fastest, so the 16 lanes storing one transposed row write 128
     // contiguous bytes (rows 8 channels apart would all hit the same banks).
     const int vkg = tid % (kBN / 4), vdg = tid / (kBN / 4);
-    // Loads go through buffer resources over this (batch, kv head)'s rows: the
-    // per-lane offsets below never change, the tile offset is a scalar, and keys
-    // past kv_len read zeros (every tile reaching past kv_len is masked anyway).
+    // Loads go through buffer resources over this (batch, kv head)'s rows. The tile
+    // offset is added to the per-lane offset (the range check covers the per-lane
+    // offset, not the scalar one), so keys past kv_len read zeros (every tile
+    // reaching past kv_len is masked anyway; a zero scale never wins a maximum).
     const __amdgpu_buffer_rsrc_t krsrc =
         buffer_rsrc(kbase, (uint32_t)((int64_t)(a.kv_len - 1) * a.k_st + D));
     const __amdgpu_buffer_rsrc_t vrsrc =
@@ -315,23 +329,23 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     const __amdgpu_buffer_rsrc_t ksrsrc = buffer_rsrc(a.ks + srow, (uint32_t)a.kv_len * 4u);
     const __amdgpu_buffer_rsrc_t vsrsrc = buffer_rsrc(a.vs + srow, (uint32_t)a.kv_len * 4u);
     auto load_tile = [&](int kt) {
-        const int ks_off = __builtin_amdgcn_readfirstlane((int)(kt * a.k_st));
-        const int vs_off = __builtin_amdgcn_readfirstlane((int)(kt * a.v_st));
+        const uint32_t ks_off = (uint32_t)__builtin_amdgcn_readfirstlane((int)(kt * a.k_st));
+        const uint32_t vs_off = (uint32_t)__builtin_amdgcn_readfirstlane((int)(kt * a.v_st));
 #pragma unroll
         for (int j = 0; j < KLOADS; ++j)
-            kreg[j] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, koff[j], ks_off, 0);
+            kreg[j] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, koff[j] + ks_off, 0, 0);
         if (tid < VBLOCKS) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const auto w = __builtin_amdgcn_raw_buffer_load_b64(vrsrc, voff[i], vs_off, 0);
+                const auto w = __builtin_amdgcn_raw_buffer_load_b64(vrsrc, voff[i] + vs_off, 0, 0);
                 vreg[i] = uint2{w[0], w[1]};
             }
         }
         if (KV_TOKEN && wave == 0) {
             ks_reg = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(ksrsrc, lane * 4, kt * 4, 0));
+                float, __builtin_amdgcn_raw_buffer_load_b32(ksrsrc, (lane + kt) * 4, 0, 0));
             vs_reg = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(vsrsrc, lane * 4, kt * 4, 0));
+                float, __builtin_amdgcn_raw_buffer_load_b32(vsrsrc, (lane + kt) * 4, 0, 0));
         }
     };
     auto store_tile = [&](int buf) {
@@ -602,9 +616,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     if (MODE == kStream && sp.parts > 1) {
         // Leave this part in its slot (every lane: rows past q_len hold finite
         // values), then count the part in; the last part of the item merges. The
-        // slot stores and loads and the counter are device-coherent accesses of
-        // their own (sc1), so no L2 write-back or invalidation is needed: the
-        // stores complete (vmcnt 0) before the workgroup's count.
+        // slot stores and loads are device-coherent atomics (sc1); every thread
+        // releases its stores at agent scope before the barrier, the counter
+        // increment is an acquire-release operation, and the merging part acquires
+        // at agent scope before it reads the other parts' slots.
         constexpr int SF = StreamSlot<D>::FLOATS, OF = StreamSlot<D>::O_FLOATS;
         constexpr int E = DB * 8;  // 8-byte elements of output per lane
         auto pack = [](float x, float y) {
@@ -627,13 +642,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                 put(so + (wave * E + d * 8 + e) * kWave + lane,
                     pack(acc[d][2 * e], acc[d][2 * e + 1]));
         put(so + OF / 2 + wave * kWave + lane, pack(m_run, l_tot));
-        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         if (tid == 0)
-            *sTicket = __hip_atomic_fetch_add(sa.counters + sp.item, 1u, __ATOMIC_RELAXED,
+            *sTicket = __hip_atomic_fetch_add(sa.counters + sp.item, 1u, __ATOMIC_ACQ_REL,
                                               __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (*sTicket != (uint32_t)(sp.parts - 1)) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (tid == 0)  // ready for the next launch
             __hip_atomic_store(sa.counters + sp.item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // Parts in order: part p is workgroup first_wg + p; the first part sits in
@@ -734,6 +750,12 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
     int tile, b, h;
     item_coords(a, grid_rank(a), tile, b, h);
+    if (!KV_TOKEN && a.item_sel != 0) {
+        const int kvh = h / (a.q_heads / a.kv_heads);
+        const bool wide = 127.0f * scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) >
+                          kPreciseAbove;
+        if (wide != (a.item_sel == 2)) return;
+    }
     prefill_body<D, KV_TOKEN, PRECISE, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
                                                StreamArgs{}, StreamPart{}, nullptr);
 }
@@ -867,29 +889,39 @@ int64_t stream_slot_floats(int64_t D) {
     return D == 128 ? StreamSlot<128>::FLOATS : StreamSlot<64>::FLOATS;
 }
 
-// Items of a launch at or below which the balanced schedule is used. With one
-// item per compute unit or fewer, a causal grid leaves most units idle for most
-// of the launch, and cutting items pays; from two items per compute unit the
-// one-item grid pairs a heavy and a light item on each unit instead, and the
-// cuts' partial results (written, counted in, merged: about 5 us per cut item)
-// cost more than the balance gains (measured on 1x32x2048x128: 60 us balanced,
-// 49 us paired).
-int64_t stream_item_limit() {
-    const char *e = getenv("REEF_PREFILL_STREAM_ITEMS");
-    return e ? atoll(e) : compute_units();
-}
 
 }  // namespace
 }  // namespace reef
 
 using namespace reef;
 
+namespace reef {
+namespace {
+// Workspace: the balanced schedule's counters and slots, then (head_dim 128) the
+// packed schedule's value image, 256-byte aligned.
+int64_t balanced_bytes(const reef_attention_params &p) {
+    return ceil_div(stream_counter_bytes(p) + 2 * stream_groups() * stream_slot_floats(p.head_dim) * 4,
+                    256) * 256;
+}
+int64_t packed_bytes(const reef_attention_params &p) {
+    return p.head_dim == 128 && p.kv_heads > 0 && p.kv_len > 0
+               ? packed_image_bytes(p.batch, p.kv_heads, p.kv_len)
+               : 0;
+}
+// The packed schedule is the library's choice for grids with at least one
+// (light, heavy) pair of 256-row query tiles per compute unit.
+bool packed_by_default(const reef_attention_params &p) {
+    const int64_t pairs = (ceil_div(p.q_len, 256) + 1) / 2 * p.batch * p.q_heads;
+    return pairs >= compute_units();
+}
+}  // namespace
+}  // namespace reef
+
 extern "C" size_t reef_attention_prefill_workspace_bytes(const reef_attention_params *p) {
     if (!p || p->batch <= 0 || p->q_heads <= 0 || p->q_len <= 0 ||
         (p->head_dim != 64 && p->head_dim != 128))
         return 0;
-    return (size_t)(stream_counter_bytes(*p) +
-                    2 * stream_groups() * stream_slot_floats(p->head_dim) * 4);
+    return (size_t)(balanced_bytes(*p) + packed_bytes(*p));
 }
 
 extern "C" reef_status reef_attention_prefill_int8(
@@ -971,8 +1003,31 @@ extern "C" reef_status reef_attention_prefill_int8(
     // The balanced schedule needs the caller's workspace; without it, small grids
     // take the persistent split kernel.
     if (workspace && !aligned(workspace, 256)) return REEF_INVALID_ARGUMENT;
-    const bool stream_ok = workspace && workspace_bytes >= reef_attention_prefill_workspace_bytes(p);
-    if (!tok && !precise && stream_ok && items <= stream_item_limit()) {
+    const uint32_t sched = p->flags & REEF_ATTN_SCHED_MASK;
+    if (sched != REEF_ATTN_SCHED_AUTO && sched != REEF_ATTN_SCHED_ONE_ITEM &&
+        sched != REEF_ATTN_SCHED_SPLIT && sched != REEF_ATTN_SCHED_BALANCED &&
+        sched != REEF_ATTN_SCHED_PACKED)
+        return REEF_INVALID_ARGUMENT;
+    const int64_t bal_bytes = balanced_bytes(*p);
+    const bool stream_ok = workspace && (int64_t)workspace_bytes >= bal_bytes;
+    const bool packed_ok = D == 128 && !tok && workspace &&
+                           (int64_t)workspace_bytes >= bal_bytes + packed_bytes(*p);
+    if (sched == REEF_ATTN_SCHED_PACKED && !packed_ok) return REEF_INVALID_ARGUMENT;
+    if (sched == REEF_ATTN_SCHED_PACKED ||
+        (sched == REEF_ATTN_SCHED_AUTO && packed_ok && packed_by_default(*p))) {
+        const int64_t qst[3] = {a.q_sb, a.q_sh, a.q_st}, kst[3] = {a.k_sb, a.k_sh, a.k_st},
+                      vst[3] = {a.v_sb, a.v_sh, a.v_st}, ost[3] = {a.o_sb, a.o_sh, a.o_st};
+        return prefill_packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out,
+                                     ost, static_cast<char *>(workspace) + bal_bytes, stream);
+    }
+    // The balanced and split schedules round P to one fp16 (11 bits); the library
+    // chooses them only when the caller forces them. The one-item kernel splits P
+    // into hi + lo where the values need it (per item, two launches).
+    if (sched == REEF_ATTN_SCHED_BALANCED && (tok || precise || !stream_ok))
+        return REEF_INVALID_ARGUMENT;
+    if (sched == REEF_ATTN_SCHED_SPLIT && (tok || precise)) return REEF_INVALID_ARGUMENT;
+    a.item_sel = 0;
+    if (sched == REEF_ATTN_SCHED_BALANCED) {
         const int64_t per_head = host_steps_before(*p, a.q_tiles - 1) +
                                  host_tile_steps(*p, a.q_tiles - 1);
         StreamArgs sa;
@@ -990,14 +1045,11 @@ extern "C" reef_status reef_attention_prefill_int8(
             hipLaunchKernelGGL(prefill_stream_kernel<64>, sgrid, dim3(kThreads), 0, stream, a, sa);
         return launch_status();
     }
-    const char *sp = getenv("REEF_PREFILL_SPLIT");
-    const bool split =
-        !tok && !precise && (sp ? atoi(sp) != 0 : items <= compute_units());
+    const bool split = sched == REEF_ATTN_SCHED_SPLIT;
     // The 4-wave kernel places two workgroups on each of the 256 compute units at
     // once; zig-zag pairs a heavy and a light tile there. The split kernel holds a
     // compute unit alone and takes the tiles heaviest first.
-    const char *zz = getenv("REEF_PREFILL_ZIGZAG");
-    a.zigzag = zz ? atoi(zz) : (!split && items <= 512 ? 1 : 0);
+    a.zigzag = !split && items <= 2 * compute_units() ? 1 : 0;
     if (split) {
         const dim3 pgrid((unsigned)std::min<int64_t>(items, compute_units()));
         if (D == 128)
@@ -1010,23 +1062,25 @@ extern "C" reef_status reef_attention_prefill_int8(
     }
 #define REEF_PREFILL_LAUNCH(DIM, TOK, PREC)                                                  \
     hipLaunchKernelGGL((prefill_kernel<DIM, TOK, PREC>), grid, dim3(kThreads), 0, stream, a)
-    if (D == 128) {
-        if (tok) {
-            if (precise) REEF_PREFILL_LAUNCH(128, true, true);
-            else REEF_PREFILL_LAUNCH(128, true, false);
+    if (tok || precise) {  // per-token K/V scales always split P
+        if (D == 128) {
+            if (tok) REEF_PREFILL_LAUNCH(128, true, true);
+            else REEF_PREFILL_LAUNCH(128, false, true);
         } else {
-            if (precise) REEF_PREFILL_LAUNCH(128, false, true);
-            else REEF_PREFILL_LAUNCH(128, false, false);
+            if (tok) REEF_PREFILL_LAUNCH(64, true, true);
+            else REEF_PREFILL_LAUNCH(64, false, true);
         }
-    } else {
-        if (tok) {
-            if (precise) REEF_PREFILL_LAUNCH(64, true, true);
-            else REEF_PREFILL_LAUNCH(64, true, false);
-        } else {
-            if (precise) REEF_PREFILL_LAUNCH(64, false, true);
-            else REEF_PREFILL_LAUNCH(64, false, false);
-        }
+        return launch_status();
     }
+    // Items whose values stay within kPreciseAbove take one fp16 P, the others the
+    // hi + lo split; each launch returns at once from the other's items.
+    a.item_sel = 1;
+    if (D == 128) REEF_PREFILL_LAUNCH(128, false, false);
+    else REEF_PREFILL_LAUNCH(64, false, false);
+    if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
+    a.item_sel = 2;
+    if (D == 128) REEF_PREFILL_LAUNCH(128, false, true);
+    else REEF_PREFILL_LAUNCH(64, false, true);
 #undef REEF_PREFILL_LAUNCH
     return launch_status();
 }

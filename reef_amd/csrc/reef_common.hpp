@@ -20,6 +20,11 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.44269504088896341f;
+// P.V precision: where dequantized values reach above this magnitude, P is split
+// into fp16 hi + lo parts; below it one fp16 P keeps the attention output within
+// 5e-4 of the fp32 result (its rounding moves an output by about 2^-12 |v_j - out|
+// per dominant key).
+constexpr float kPreciseAbove = 6.0f;
 
 // --- matrix instructions ---------------------------------------------------------------
 // Output layout of the 32x32 instructions: lane l holds column l % 32 and, in

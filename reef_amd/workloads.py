@@ -114,8 +114,8 @@ class DecodeConfig:
         tokens = int(np.sum(L)) * self.kv_heads
         D = self.head_dim
         b = tokens * (2 * D + 2 * 4)
-        b += self.batch * self.q_heads * (D + 4)        # q int8 + per-(b, h) scale
-        b += self.batch * self.q_heads * D * 4          # fp32 out
+        b += self.batch * self.q_heads * D + self.q_heads * 4   # q int8 + per-head scales
+        b += self.batch * self.q_heads * D * 4                  # fp32 out
         if self.paged:
             b += 4 * int(np.sum((L + 15) // 16))
         return b

@@ -76,8 +76,15 @@ def test_prefill_workspace_bytes_and_alignment():
     p = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048)
     n = lib.reef_attention_prefill_workspace_bytes(C.byref(p))
     # item counters (512 items), then two partial slots per workgroup, two workgroups per
-    # compute unit (256 without a GPU): 128 x 128 outputs plus (max, sum) of 128 rows
-    assert n == 2048 + 2 * 512 * (128 * 128 + 2 * 256) * 4
+    # compute unit (256 without a GPU): 128 x 128 outputs plus (max, sum) of 128 rows;
+    # then the packed value image: 32 tiles of 64 keys per head, 16 KB each, and one
+    # 4-byte block maximum per tile
+    balanced = 2048 + 2 * 512 * (128 * 128 + 2 * 256) * 4
+    image = 32 * 32 * 16384 + 32 * 32 * 4
+    assert n == balanced + image
+    p64 = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048, head_dim=64)
+    assert lib.reef_attention_prefill_workspace_bytes(C.byref(p64)) == \
+        2048 + 2 * 512 * (128 * 64 + 2 * 256) * 4  # no packed schedule at head_dim 64
     assert lib.reef_attention_prefill_workspace_bytes(C.byref(good_params(head_dim=96))) == 0
     assert lib.reef_attention_prefill_workspace_bytes(None) == 0
     # a workspace that is not 256-byte aligned

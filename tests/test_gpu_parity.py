@@ -162,6 +162,21 @@ def test_quantize_rows_with_row_stride(reef):
     assert np.array_equal(host(q), qo) and np.array_equal(host(s), so)
 
 
+@pytest.mark.parametrize("n,group", [(4096 * 128, 128), (1_000_003, 1_000_003), (77, 7),
+                                     (3 * 8193, 8193), (4 * 61, 61), (1, 1), (10, 4)])
+def test_dequantize_bit_exact(reef, n, group):
+    """float(code) * scale[i / group], bit for bit: per-token rows (group = width),
+    one scale over the tensor (group = n), odd sizes, groups that are not multiples
+    of 4 (the scalar kernel), and a short last group."""
+    case(f"dequantize n={n} group={group}")
+    rng = np.random.default_rng(n + group)
+    q = rand_i8(rng, (n,), low=-128)
+    scales = rng.uniform(1e-4, 3.0, (n + group - 1) // group).astype(np.float32)
+    x = host(reef.dequantize(gpu(q), gpu(scales), group))
+    want = oracle.dequantize(q, scales, group)
+    assert np.array_equal(x.view(np.uint32), want.view(np.uint32))
+
+
 def test_quantize_rejects_non_finite(reef):
     case("quantize non-finite -> NonFiniteInput")
     for bad in (math.nan, math.inf, -math.inf):
@@ -186,7 +201,7 @@ def _quantize(x, gran):
     return oracle.quantize_per_token(x)
 
 
-def _run_prefill(reef, q, k, v, p, precise=False, workspace=None):
+def _run_prefill(reef, q, k, v, p, precise=False, workspace=None, schedule=0):
     qq, qs = _quantize(q, p.q_granularity)
     kq, ks = _quantize(k, p.kv_granularity)
     vq, vs = _quantize(v, p.kv_granularity)
@@ -194,7 +209,7 @@ def _run_prefill(reef, q, k, v, p, precise=False, workspace=None):
                                  query_start=p.start(), window=p.window,
                                  softmax_scale=p.softmax_scale, q_granularity=p.q_granularity,
                                  kv_granularity=p.kv_granularity, precise=precise,
-                                 workspace=workspace)
+                                 workspace=workspace, schedule=schedule)
     gold = oracle.attention_int8(p, qq, kq, vq, qs, ks, vs)
     return host(out), gold
 
@@ -228,6 +243,10 @@ PREFILL_CASES = [
     # very large log2-domain score scales: rows dominated by one key (peaked softmax)
     (1, 2, 2, 256, 256, 128, None, 0, 1, 1, 3000.0),
     (1, 2, 1, 200, 300, 64, None, 0, 0, 0, 20000.0),
+    # window past the first key tiles of a long prefix, GQA 2:1, head_dim 128
+    (1, 4, 2, 300, 700, 128, 250, 90, 1, 1, None),
+    # several 256-row query tiles and an odd tile count (a middle tile without a pair)
+    (2, 3, 3, 1200, 1200, 128, None, 0, 1, 1, None),
 ]
 
 
@@ -245,20 +264,82 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
     p = oracle.Problem(B, Hq, Hkv, Sq, Skv, D, query_start=start, window=window,
                        softmax_scale=(1 / math.sqrt(D)) if scale is None else scale,
                        q_granularity=gq, kv_granularity=gkv)
-    # both fp16 P and split P; the balanced schedule (with a workspace), and without
-    # one the one-item-per-workgroup and the persistent key-split kernels (chosen by
-    # size, forced here through REEF_PREFILL_SPLIT)
-    for precise, split, ws in ((False, "0", None), (False, "0", False), (False, "1", False),
-                               (True, "0", None)):
-        os.environ["REEF_PREFILL_SPLIT"] = split
-        try:
-            out, gold = _run_prefill(reef, q, k, v, p, precise, workspace=ws)
-        finally:
-            del os.environ["REEF_PREFILL_SPLIT"]
+    # both fp16 P and split P; the library's choice with and without a workspace, and
+    # every schedule forced through the flags (the split and balanced schedules do
+    # not take per-token K/V scales)
+    runs = [(False, reef.SCHED_AUTO, None), (False, reef.SCHED_AUTO, False),
+            (False, reef.SCHED_ONE_ITEM, False), (True, reef.SCHED_AUTO, None)]
+    if gkv != 2:
+        runs += [(False, reef.SCHED_SPLIT, False), (False, reef.SCHED_BALANCED, None)]
+        if D == 128:
+            runs += [(False, reef.SCHED_PACKED, None), (True, reef.SCHED_PACKED, None)]
+    for precise, sched, ws in runs:
+        out, gold = _run_prefill(reef, q, k, v, p, precise, workspace=ws, schedule=sched)
         err = np.abs(out - gold).max()
-        print(f"precise={precise} split={split} workspace={ws is not False} "
+        print(f"precise={precise} schedule={sched:#x} workspace={ws is not False} "
               f"max_abs_err {err:.3e}", flush=True)
-        assert err <= TOL, (precise, split, ws, err)
+        assert err <= TOL, (precise, sched, ws, err)
+
+
+def test_prefill_outlier_channels(reef):
+    """Per-head scales with a few value channels scaled x8 (activation outliers):
+    the values of those heads reach |v| ~ 30, where one fp16 P is not precise enough.
+    Every schedule the library chooses by itself (packed with a workspace, the
+    one-item kernel without) and the forced precise split stay within TOL."""
+    B, H, S, D = 1, 4, 1100, 128
+    case(f"prefill outlier channels B{B} H{H} S{S} D{D}")
+    q = W.lcg_normal(801, B * H * S * D).reshape(B, H, S, D)
+    k = W.lcg_normal(802, B * H * S * D).reshape(B, H, S, D)
+    v = W.lcg_normal(803, B * H * S * D).reshape(B, H, S, D)
+    for h, c in ((0, 5), (1, 70), (1, 100), (3, 127)):
+        for t in (q, k, v):
+            t[:, h, :, c] *= 8.0
+    p = oracle.Problem(B, H, H, S, S, D, softmax_scale=1 / math.sqrt(D))
+    runs = [(False, reef.SCHED_AUTO, None), (False, reef.SCHED_AUTO, False),
+            (False, reef.SCHED_PACKED, None), (False, reef.SCHED_ONE_ITEM, False),
+            (True, reef.SCHED_ONE_ITEM, False)]
+    for precise, sched, ws in runs:
+        out, gold = _run_prefill(reef, q, k, v, p, precise, workspace=ws, schedule=sched)
+        err = np.abs(out - gold).max()
+        print(f"precise={precise} schedule={sched:#x} workspace={ws is not False} "
+              f"max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL, (precise, sched, ws, err)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,gran", [(1, 8, 2, 300, 128, 1), (2, 4, 4, 130, 64, 0),
+                                               (1, 4, 1, 77, 128, 2)])
+def test_prefill_projection_layout_strides(reef, B, Hq, Hkv, S, D, gran):
+    """q, k and v read in place from projection outputs [B, S, H * D] (strides
+    {S H D, D, H D}, the engine's [len, heads * head_dim] rows) and the output written
+    into an [B, S, Hq * D] buffer: the same result as packed heads."""
+    case(f"prefill strided projection layout B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} gran{gran}")
+    seed = 900 + S + D
+    q = W.lcg_normal(seed, B * Hq * S * D).reshape(B, Hq, S, D)
+    k = W.lcg_normal(seed + 1, B * Hkv * S * D).reshape(B, Hkv, S, D)
+    v = W.lcg_normal(seed + 2, B * Hkv * S * D).reshape(B, Hkv, S, D)
+    qq, qs = _quantize(q, gran)
+    kq, ks = _quantize(k, gran)
+    vq, vs = _quantize(v, gran)
+    p = oracle.Problem(B, Hq, Hkv, S, S, D, softmax_scale=1 / math.sqrt(D), q_granularity=gran,
+                       kv_granularity=gran)
+    gold = oracle.attention_int8(p, qq, kq, vq, qs, ks, vs)
+
+    def proj(x):  # [B, H, S, D] -> a [B, H, S, D] view of a [B, S, H * D] buffer
+        Bx, H, Sx, Dx = x.shape
+        buf = gpu(np.ascontiguousarray(x.transpose(0, 2, 1, 3)).reshape(Bx, Sx, H * Dx))
+        return buf.view(Bx, Sx, H, Dx).permute(0, 2, 1, 3)
+
+    qv, kv_, vv = proj(qq), proj(kq), proj(vq)
+    assert qv.stride() == (S * Hq * D, D, Hq * D, 1)
+    obuf = torch.full((B, S, Hq * D), float("nan"), device="cuda")
+    out = obuf.view(B, S, Hq, D).permute(0, 2, 1, 3)
+    for sched in (reef.SCHED_AUTO, reef.SCHED_ONE_ITEM):
+        reef.attention_prefill(qv, kv_, vv, gpu(qs), gpu(ks), gpu(vs), q_granularity=gran,
+                               kv_granularity=gran, out=out, schedule=sched)
+        got = host(out)
+        err = np.abs(got - gold).max()
+        print(f"schedule={sched:#x} max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL
 
 
 STREAM_CASES = [
@@ -385,6 +466,28 @@ def test_decode_contiguous_matches_oracle(reef, B, Hq, Hkv, D, lens, window, spl
                                 gpu(np.array(lens, np.int32)), window=window,
                                 softmax_scale=scale, num_splits=splits)
     gold = _decode_gold(qq, qs, kq, ks, vq, vs, lens, window, scale)
+    err = np.abs(host(out) - gold).max()
+    print(f"max_abs_err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def test_decode_per_head_query_scales(reef):
+    """q quantized with one scale per query head over the whole batch (PER_HEAD), the
+    setting of the B64 32q/8kv decode workload, against the oracle with the same
+    per-head scales."""
+    B, Hq, Hkv, D, lens = 6, 32, 8, 128, [640, 1, 333, 640, 129, 17]
+    max_ctx = 640
+    case(f"decode per-head q scales B{B} Hq{Hq} Hkv{Hkv} lens{lens}")
+    _, _, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 71, max_ctx)
+    qf = W.lcg_normal(72, B * Hq * D).reshape(B, Hq, 1, D)
+    qf[:, 5] *= 9.0
+    qq, qs_head = oracle.quantize_per_head(qf)
+    qq = qq.reshape(B, Hq, D)
+    scale = 1 / math.sqrt(D)
+    out = reef.attention_decode(gpu(qq), gpu(qs_head), gpu(kq), reef.pack_v_pages(gpu(vq)),
+                                gpu(ks), gpu(vs), gpu(np.array(lens, np.int32)),
+                                softmax_scale=scale, q_granularity=reef.PER_HEAD)
+    gold = _decode_gold(qq, np.broadcast_to(qs_head, (B, Hq)), kq, ks, vq, vs, lens, 0, scale)
     err = np.abs(host(out) - gold).max()
     print(f"max_abs_err {err:.3e}", flush=True)
     assert err <= TOL

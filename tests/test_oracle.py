@@ -67,6 +67,32 @@ def test_quantize_rows_known_answer():
     assert s[2] == np.float32(1.0) / np.float32(127.0) and q[2, 0] == 127
 
 
+def test_dequantize_known_answers_and_round_trip():
+    """static_cast<float>(code) * scale (test_int8.cpp:182). Pinned by the
+    quantize_rows known answer of test_quant.cpp:56-74 read back ([127, 64, -64] at
+    scale 2 is [254, 128, -128]), by the round-trip bound |x - deq(q(x))| <= s / 2
+    on every value (a wrong scale index, a dropped scale or a sign flip breaks it),
+    and by codes times powers of two, which are exact."""
+    q, s = oracle.quantize_rows(np.array([[254.0, 127.0, -127.0]], np.float32))
+    assert np.array_equal(oracle.dequantize(q, s, 3), np.array([254, 128, -128], np.float32))
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((37, 53)) * rng.uniform(0.01, 40.0, (37, 1))).astype(np.float32)
+    x[3] = 0.0
+    q, s = oracle.quantize_rows(x)
+    back = oracle.dequantize(q, s, 53).reshape(37, 53)
+    bound = s.astype(np.float64)[:, None] * (0.5 + 1e-6)
+    assert np.all(np.abs(back.astype(np.float64) - x) <= bound)
+    assert not back[3].any()
+    codes = np.arange(-128, 128, dtype=np.int8)
+    scales = np.float32(2.0) ** np.arange(-20, 12, dtype=np.float32)  # 32 groups of 8
+    got = oracle.dequantize(codes, scales, 8)
+    want = codes.astype(np.float64) * np.repeat(scales.astype(np.float64), 8)
+    assert np.array_equal(got.astype(np.float64), want)
+    # a tail group shorter than the others
+    got = oracle.dequantize(codes[:13], np.array([0.5, 3.0], np.float32), 8)
+    assert np.array_equal(got[8:], codes[8:13].astype(np.float32) * np.float32(3.0))
+
+
 def test_w8a8_golden_pins_per_row_quantization(golden_dir):
     """The engine's W8A8 projection golden (linear.hpp:106-132) is reproduced bit
     for bit by oracle.quantize_rows + exact int32 sums + float(sum) * (s_row * s_col).
