@@ -273,6 +273,23 @@ reef_status reef_attention_decode_int8_paged(
     const int32_t *context_lens, float *out, void *workspace, size_t workspace_bytes,
     uint32_t *status_word, hipStream_t stream);
 
+/* Allocation-free form of reef_attention_decode_int8_paged, with no counterpart in
+ * the reference: for callers that cannot allocate or pass device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * split-merge workspace is a fixed 8 MiB array inside the library, one per GPU,
+ * held until the process ends; a call whose workspace
+ * (reef_attention_decode_workspace_bytes) would exceed it returns REEF_UNSUPPORTED
+ * before any launch. Each call clears the counters it uses with a small fill
+ * kernel on `stream`, then runs the same kernels as the workspace entry point
+ * (bit-identical outputs). Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other host threads) race and must not run
+ * concurrently. Nothing is allocated or freed. */
+reef_status reef_attention_decode_int8_paged_noalloc(
+    const reef_decode_params *p, const int8_t *q, const float *q_scales, const int8_t *k_pages,
+    const int8_t *v_pages, const float *k_scale_pages, const float *v_scale_pages,
+    const int32_t *block_table, int64_t max_blocks_per_seq, int64_t num_pages,
+    const int32_t *context_lens, float *out, uint32_t *status_word, hipStream_t stream);
+
 /* Token-major values [pages * 16, D] (page-contiguous) -> transposed pages
  * [pages, D, 16]. */
 reef_status reef_kv_pack_v_pages(const int8_t *v_tokens, int64_t pages, int64_t head_dim,

@@ -34,7 +34,8 @@ EXPORTS = [
     "reef_quantize_int8_per_token", "reef_dequantize_int8", "reef_read_status_word",
     "reef_attention_prefill_workspace_bytes", "reef_attention_prefill_int8", "reef_qk_scores_i32",
     "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
-    "reef_attention_decode_int8_paged", "reef_kv_pack_v_pages", "reef_kv_append_int8",
+    "reef_attention_decode_int8_paged", "reef_attention_decode_int8_paged_noalloc",
+    "reef_kv_pack_v_pages", "reef_kv_append_int8",
     "reef_kv_append_int8_paged", "reef_attention_int8_integer", "reef_linear_w8a8_workspace_bytes",
     "reef_linear_w8a8", "reef_gemm_w8a8",
 ]
@@ -116,6 +117,8 @@ _SIGS = {
                                    C.c_size_t, _P, _P],
     "reef_attention_decode_int8_paged": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P,
                                          _I64, _I64, _P, _P, _P, C.c_size_t, _P, _P],
+    "reef_attention_decode_int8_paged_noalloc": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P,
+                                                 _P, _I64, _I64, _P, _P, _P, _P],
     "reef_kv_pack_v_pages": [_P, _I64, _I64, _P, _P],
     "reef_linear_w8a8_workspace_bytes": [_I64, _I64],
     "reef_linear_w8a8": [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, C.c_size_t, _P,

@@ -23,6 +23,7 @@
 // 4:1 grouping); the instructions are far from the bound, HBM is.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "reef_common.hpp"
 
@@ -547,9 +548,9 @@ int default_splits(const reef_decode_params *p) {
     return (int)std::max<int64_t>(1, s);
 }
 
-reef_status validate(const reef_decode_params *p, const int8_t *q, const float *q_scales,
-                     float *out, void *workspace, size_t workspace_bytes) {
-    if (!p || !q || !q_scales || !out || !workspace) return REEF_INVALID_ARGUMENT;
+reef_status validate_params(const reef_decode_params *p, const int8_t *q, const float *q_scales,
+                            float *out) {
+    if (!p || !q || !q_scales || !out) return REEF_INVALID_ARGUMENT;
     if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->max_context <= 0 ||
         p->q_heads % p->kv_heads != 0 || p->window < 0 || p->num_splits < 0 ||
         p->max_context % kPage != 0 || !std::isfinite(p->softmax_scale) ||
@@ -560,8 +561,17 @@ reef_status validate(const reef_decode_params *p, const int8_t *q, const float *
     if (p->q_heads / p->kv_heads > 16 || p->kv_heads > 65535 || p->batch > 65535 ||
         p->max_context >= (int64_t(1) << 30))
         return REEF_UNSUPPORTED;
-    if (!aligned(q, 16) || !aligned(out, 4) || !aligned(workspace, 16)) return REEF_INVALID_ARGUMENT;
-    if (workspace_bytes < reef_attention_decode_workspace_bytes(p)) return REEF_INVALID_ARGUMENT;
+    if (!aligned(q, 16) || !aligned(out, 4)) return REEF_INVALID_ARGUMENT;
+    return REEF_OK;
+}
+
+reef_status validate(const reef_decode_params *p, const int8_t *q, const float *q_scales,
+                     float *out, void *workspace, size_t workspace_bytes) {
+    const reef_status st = validate_params(p, q, q_scales, out);
+    if (st != REEF_OK) return st;
+    if (!workspace || !aligned(workspace, 16) ||
+        workspace_bytes < reef_attention_decode_workspace_bytes(p))
+        return REEF_INVALID_ARGUMENT;
     return REEF_OK;
 }
 
@@ -639,6 +649,42 @@ extern "C" reef_status reef_attention_decode_int8(const reef_decode_params *p, c
     return launch_decode<false>(p, a, out, workspace, stream);
 }
 
+namespace reef {
+namespace {
+
+// The allocation-free paged decode keeps its workspace (counters and part slots)
+// in this file-scope array: one copy per GPU, held until the process ends, shared
+// by every call on that GPU. In host code `scratch` is a stand-in symbol, not a
+// device address: scratch_address() resolves the device address once per device
+// (with that device current) and every use goes through it.
+constexpr int64_t kScratchBytes = int64_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void *scratch_ptr[kMaxDevices];
+
+void *scratch_address() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        scratch_ptr[dev] = ptr;
+    }
+    return scratch_ptr[dev];
+}
+
+__global__ void clear_words(uint32_t *words, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        words[i] = 0;
+}
+
+}  // namespace
+}  // namespace reef
+
 extern "C" reef_status reef_attention_decode_int8_paged(
     const reef_decode_params *p, const int8_t *q, const float *q_scales, const int8_t *k_pages,
     const int8_t *v_pages, const float *k_scale_pages, const float *v_scale_pages,
@@ -666,6 +712,30 @@ extern "C" reef_status reef_attention_decode_int8_paged(
     a.max_blocks = (int32_t)max_blocks_per_seq;
     a.num_pages = (int32_t)num_pages;
     return launch_decode<true>(p, a, out, workspace, stream);
+}
+
+extern "C" reef_status reef_attention_decode_int8_paged_noalloc(
+    const reef_decode_params *p, const int8_t *q, const float *q_scales, const int8_t *k_pages,
+    const int8_t *v_pages, const float *k_scale_pages, const float *v_scale_pages,
+    const int32_t *block_table, int64_t max_blocks_per_seq, int64_t num_pages,
+    const int32_t *context_lens, float *out, uint32_t *status_word, hipStream_t stream) {
+    // Shapes and pointers are checked before the scratch address is looked up.
+    const reef_status st = validate_params(p, q, q_scales, out);
+    if (st != REEF_OK) return st;
+    const int64_t need = workspace_bytes(p);
+    if (need > kScratchBytes) return REEF_UNSUPPORTED;  // beyond the fixed scratch array
+    void *ws = scratch_address();
+    if (!ws) return REEF_HIP_ERROR;
+    // The counters must start at zero; a fill kernel (no memset node under graph
+    // capture) clears them. The part slots are written before they are read.
+    const int64_t words = counter_bytes(p) / 4;
+    hipLaunchKernelGGL(clear_words, dim3((unsigned)std::min<int64_t>(ceil_div(words, 256), 1024)),
+                       dim3(256), 0, stream, static_cast<uint32_t *>(ws), words);
+    if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
+    return reef_attention_decode_int8_paged(p, q, q_scales, k_pages, v_pages, k_scale_pages,
+                                            v_scale_pages, block_table, max_blocks_per_seq,
+                                            num_pages, context_lens, out, ws, (size_t)need,
+                                            status_word, stream);
 }
 
 extern "C" reef_status reef_kv_pack_v_pages(const int8_t *v_tokens, int64_t pages,
