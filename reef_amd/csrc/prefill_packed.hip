@@ -12,12 +12,14 @@
 //     is an fp16 integer, so the image is exact. Beside it, per tile, the largest
 //     |code| in each 32-channel block.
 //   * The attention kernel copies K (the caller's int8 rows) and the V image into
-//     LDS with direct-to-LDS buffer loads: three stages, one barrier per tile, the
-//     loads of tile j + 2 in flight while tile j computes.
-//   * A workgroup is 8 waves x 32 query rows. Per 64-key tile a wave computes
-//     S^T = K . Q^T on v_mfma_i32_32x32x32_i8 (K rows permuted so that each lane's
-//     scores are the P operand of the next step), an fp32 online softmax in base 2
-//     with a lazy rescale, and O^T = V^T . P^T on v_mfma_f32_32x32x16_f16.
+//     LDS with direct-to-LDS buffer loads: a ring of three K slots and one of three
+//     V slots, one barrier per tile, two tiles in flight beyond the one computed.
+//   * A workgroup is 4 waves x 32 query rows, two workgroups per compute unit. Per
+//     64-key tile a wave computes S^T = K . Q^T on v_mfma_i32_32x32x32_i8 (K rows
+//     permuted so that each lane's scores are the P operand of the next step), an
+//     fp32 online softmax in base 2 with a lazy rescale, and O^T = V^T . P^T on
+//     v_mfma_f32_32x32x16_f16. The scores of tile j + 1 are issued before tile j's
+//     softmax so the matrix cores and the vector ALU work side by side.
 //   * Precision of P: for a value block whose dequantized magnitudes reach above
 //     kPreciseAbove, P is split into fp16 hi + lo parts (two products, 22 bits);
 //     below it, P is one fp16 (11 bits). The rounding of P moves an output by about
@@ -52,13 +54,17 @@ constexpr int kPK = 64;                    // keys per tile
 constexpr int kPD = 128;                   // head_dim of this path
 constexpr int kKTile = kPK * kPD;          // int8 K bytes per tile
 constexpr int kVTile = kPK * kPD * 2;      // fp16 V image bytes per tile
-constexpr int kStage = kKTile + kVTile;    // 24 KB
-constexpr int kStages = 3;
-constexpr int kBlocks1K = kStage / 1024;   // 1 KB direct-load blocks per tile (8 K + 16 V)
+constexpr int kWaves = 4;                  // waves (32 query rows each) per workgroup
+constexpr int kBM = 32 * kWaves;           // query rows per tile
+// LDS: a ring of 3 K slots and a ring of 3 V slots. Tile j's values are read while
+// tile j + 1's keys are read (the scores of the next tile are computed one tile
+// ahead), and both rings keep two more tiles in flight.
+constexpr int kSlots = 3;
+constexpr int kKRing = kSlots * kKTile, kVRing = kSlots * kVTile;  // 24 KB + 48 KB
+constexpr int kKBlocks = kKTile / 1024 / kWaves;  // 1 KB direct loads per wave: K tile
+constexpr int kVBlocks = kVTile / 1024 / kWaves;  //                             V tile
 constexpr int kXcdCount = 8;               // workgroup i of a launch runs on XCD i % 8
-#ifndef REEF_PACKED_WAVES
-#define REEF_PACKED_WAVES 4                // waves (of 32 query rows) per workgroup: 4 or 8
-#endif
+constexpr int kPerCu = 2;                  // resident workgroups per compute unit (2 x 72 KB)
 
 // Position of 16-byte chunk c in a 128-byte LDS row r: the 16 lanes that read
 // chunk c of 16 consecutive rows land in 16 distinct bank groups.
@@ -175,45 +181,111 @@ __device__ __forceinline__ float scale_at(const float *s, int gran, int b, int h
     return s[((int64_t)b * heads + h) * tokens + t];
 }
 
-template <int WAVES>
-struct PackedShape {
-    static constexpr int BM = 32 * WAVES;                 // query rows per tile
-    static constexpr int PER_WAVE = kBlocks1K / WAVES;    // direct loads per wave and tile
-    static constexpr int K_LOADS = (kKTile / 1024) / WAVES;  // of which K blocks
-    static_assert(kBlocks1K % WAVES == 0 && (kKTile / 1024) % WAVES == 0, "loads split evenly");
-};
+// Scores accumulated from the float bias 1.5 * 2^23 (BIAS) read directly as floats:
+// the int32 sum 0x4B400000 + s is the bit pattern of 12582912 + s for |s| < 2^22
+// (|q.k| <= 128 * 128 * 128 = 2^21). The running max then lives in the same biased
+// log2 domain, m = (12582912 + s_max) c, and p = exp2((12582912 + s) c - m) is the
+// same probability up to one rounding of m, a factor common to a row that the row
+// sum cancels (rescales use differences of such m, exact by Sterbenz).
+constexpr int32_t kScoreBias = 0x4B400000;
+template <bool BIAS>
+__device__ __forceinline__ float score_float(int32_t x) {
+    return BIAS ? __int_as_float(x) : (float)x;
+}
 
-// One query tile of one (batch, head). LO: some value block splits P into hi + lo
-// (pmask bit d: channels 32d .. 32d + 31).
-template <int WAVES, bool LO>
-__device__ __forceinline__ void packed_tile(const PackedArgs &a, int b, int h, int tile,
-                                            int8_t *smem, uint32_t pmask) {
-    using S = PackedShape<WAVES>;
-    constexpr int BM = S::BM;
+// Row sums on the matrix core: v_mfma_f32_16x16x32_f16 with A = a 0/1 pattern and
+// B = the 32 x 16 P operand, whose lane 16g + n holds row n (g = 0, 2) or row
+// 16 + n (g = 1, 3) of the score block. A row 0 sums the groups of rows 0-15, A
+// row 1 those of rows 16-31: lane n (< 16) accumulates row n in register 0 and row
+// 16 + n in register 1 (the other lanes' registers stay zero).
+__device__ __forceinline__ f16x8 row_sum_pattern(int lane) {
+    const int m = lane & 15, g = lane >> 4;
+    const bool one = (m == 0 && (g & 1) == 0) || (m == 1 && (g & 1) == 1);
+    const _Float16 v = one ? (_Float16)1.0f : (_Float16)0.0f;
+    return f16x8{v, v, v, v, v, v, v, v};
+}
+// The row sum of this lane's row (lane % 32) from the accumulator above.
+__device__ __forceinline__ float row_sum_of_lane(const f32x4 &rs, int lane) {
+    const int col = lane & 31;
+    const float r0 = __shfl(rs[0], col & 15), r1 = __shfl(rs[1], col & 15);
+    return col < 16 ? r0 : r1;
+}
+// Scale the row sums by this lane's row factor (lanes 0-15 hold rows n and 16 + n).
+__device__ __forceinline__ void scale_row_sums(f32x4 &rs, float alpha, int lane) {
+    const float upper = __shfl(alpha, (lane & 15) | 16);
+    rs[0] *= alpha;
+    rs[1] *= upper;
+}
+
+// One query tile (128 rows) of one (batch, head), one wave per 32 rows. LO: some
+// value block splits P into hi + lo (pmask bit d: channels 32d .. 32d + 31). BIAS:
+// see kScoreBias. Per key tile j the wave issues the scores of tile j + 1 on the
+// matrix cores first and then runs tile j's softmax on the vector ALU, so the two
+// overlap; tile j's P.V follows. Not inlined: each variant's loop has the whole
+// scalar register file (inlined into the item loop, the variants' scalars spilled).
+// Arguments of a called function arrive in vector registers; the tile function
+// moves every launch-wide value back to scalar registers so that buffer
+// descriptors and LDS destinations stay scalar (no per-lane loops).
+__device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float uni(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int32_t, x)));
+}
+__device__ __forceinline__ int64_t uni(int64_t x) {
+    const uint64_t u = (uint64_t)x;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+template <class T>
+__device__ __forceinline__ T *uni(T *p) {
+    return reinterpret_cast<T *>(uni((int64_t)reinterpret_cast<uintptr_t>(p)));
+}
+
+__device__ __forceinline__ PackedArgs uniform_args(const PackedArgs &x) {
+    PackedArgs a;
+    a.q = uni(x.q); a.k = uni(x.k); a.img = uni(x.img); a.bmax = uni(x.bmax);
+    a.qs = uni(x.qs); a.ks = uni(x.ks); a.vs = uni(x.vs); a.out = uni(x.out);
+    a.q_sb = uni(x.q_sb); a.q_sh = uni(x.q_sh); a.q_st = uni(x.q_st);
+    a.k_sb = uni(x.k_sb); a.k_sh = uni(x.k_sh); a.k_st = uni(x.k_st);
+    a.o_sb = uni(x.o_sb); a.o_sh = uni(x.o_sh); a.o_st = uni(x.o_st);
+    a.batch = uni(x.batch); a.q_heads = uni(x.q_heads); a.kv_heads = uni(x.kv_heads);
+    a.q_len = uni(x.q_len); a.kv_len = uni(x.kv_len); a.query_start = uni(x.query_start);
+    a.window = uni(x.window); a.score_scale = uni(x.score_scale);
+    a.q_gran = uni(x.q_gran); a.kv_gran = uni(x.kv_gran); a.kv_tiles = uni(x.kv_tiles);
+    a.q_tiles = uni(x.q_tiles); a.per_head = uni(x.per_head); a.items = uni(x.items);
+    a.all_precise = uni(x.all_precise);
+    return a;
+}
+
+template <bool LO, bool BIAS>
+__device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, int b_in, int h_in,
+                                                      int tile_in, int8_t *smem_in,
+                                                      uint32_t pmask_in) {
+    const PackedArgs a = uniform_args(args);
+    const int b = uni(b_in), h = uni(h_in), tile = uni(tile_in);
+    int8_t *const smem = uni(smem_in);
+    const uint32_t pmask = (uint32_t)uni((int32_t)pmask_in);
     constexpr int DB = kPD / 32;
     constexpr float kLazy = 8.0f;  // the running max moves when a row max grows by > 2^8
+    constexpr int32_t kMasked = BIAS ? 0 : INT32_MIN;  // below every score
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, grp = lane >> 5;
     const int kvh = h / (a.q_heads / a.kv_heads);
-    const int q0 = tile * BM;
+    const int q0 = tile * kBM;
     const int row = q0 + wave * 32 + col;
     const bool row_ok = row < a.q_len;
 
-    // Visible keys of this lane's row [lo, hi], of the workgroup and of the wave.
+    // Visible keys of this lane's row [lo, hi]; keys every row of the wave sees.
     const int pos = a.query_start + row;
     const int lo = a.window > 0 ? max(0, pos + 1 - a.window) : 0;
     const int hi = min(pos, a.kv_len - 1);
-    const int r_last = min(q0 + BM, a.q_len) - 1;
+    const int w_first = q0 + wave * 32, w_last = min(w_first + 31, a.q_len - 1);
+    const int full_lo = a.window > 0 ? a.query_start + w_last + 1 - a.window : 0;
+    const int full_hi = w_first < a.q_len ? min(a.query_start + w_first, a.kv_len - 1) : -1;
+    const int r_last = min(q0 + kBM, a.q_len) - 1;
     const int key_lo = a.window > 0 ? max(0, a.query_start + q0 + 1 - a.window) : 0;
     const int key_hi = min(a.query_start + r_last, a.kv_len - 1);
-    const int w_first = q0 + wave * 32;
-    const int w_last = min(w_first + 31, a.q_len - 1);
-    const bool wave_active = w_first < a.q_len;
-    const int wk_lo = a.window > 0 ? max(0, a.query_start + w_first + 1 - a.window) : 0;
-    const int wk_hi = min(a.query_start + w_last, a.kv_len - 1);
-    const int full_lo = a.window > 0 ? a.query_start + w_last + 1 - a.window : 0;
-    const int full_hi = min(a.query_start + w_first, a.kv_len - 1);
     const int kt0 = key_lo / kPK * kPK;
     const int n_tiles = (key_hi - kt0) / kPK + 1;
 
@@ -226,42 +298,46 @@ __device__ __forceinline__ void packed_tile(const PackedArgs &a, int b, int h, i
             qop[t] = row_ok ? *reinterpret_cast<const i32x4 *>(qrow + 32 * t + 16 * grp)
                             : i32x4{0, 0, 0, 0};
     }
-    const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float ck = scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
     const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float c = cq * ck * a.score_scale;  // log2-domain score per unit of int32 sum
 
-    // Direct loads: wave w fills 1 KB blocks w, w + WAVES, ... of a stage (blocks
-    // 0-7 are K, 8-23 the V image). Lane L of K block kb writes LDS row
-    // 8 kb + L / 8 at position L % 8, which holds chunk swz(row, L % 8) of the key
-    // that the row stands for.
-    uint32_t loff[S::PER_WAVE];
+    // Direct loads: wave w fills 1 KB blocks w, w + 4, ... of a K tile and of a V
+    // tile. Lane L of K block kb writes LDS row 8 kb + L / 8 at position L % 8,
+    // which holds chunk swz(row, L % 8) of the key that the row stands for.
+    uint32_t koff[kKBlocks], voff[kVBlocks];
 #pragma unroll
-    for (int i = 0; i < S::PER_WAVE; ++i) {
-        const int blk = wave + WAVES * i;
-        if (i < S::K_LOADS) {
-            const int r = 8 * blk + lane / 8;
-            const int key = 32 * (r >> 5) + key_of_row32(r & 31);
-            loff[i] = (uint32_t)(key * a.k_st + 16 * swz(r, lane & 7));
-        } else {
-            loff[i] = (uint32_t)(16 * (64 * (blk - kKTile / 1024) + lane));
-        }
+    for (int i = 0; i < kKBlocks; ++i) {
+        const int r = 8 * (wave + kWaves * i) + lane / 8;
+        const int key = 32 * (r >> 5) + key_of_row32(r & 31);
+        koff[i] = (uint32_t)(key * a.k_st + 16 * swz(r, lane & 7));
     }
+#pragma unroll
+    for (int i = 0; i < kVBlocks; ++i) voff[i] = (uint32_t)(16 * (64 * (wave + kWaves * i) + lane));
     const int8_t *kbase = a.k + b * a.k_sb + kvh * a.k_sh;
     const int8_t *ibase = a.img + ((int64_t)(b * a.kv_heads + kvh) * a.kv_tiles) * kVTile;
-    auto issue = [&](int j) {  // tile j into stage j % kStages
+    int8_t *kring = smem, *vring = smem + kKRing;
+    auto issue_k = [&](int j) {  // K of tile j into K slot j % 3; rows past kv_len read zeros
         const int kt = kt0 + kPK * j;
-        int8_t *st = smem + (j % kStages) * kStage;
-        // The tile's K rows as their own buffer range: rows past kv_len read zeros.
         const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(
             kbase + (int64_t)kt * a.k_st, (uint32_t)((int64_t)(a.kv_len - 1 - kt) * a.k_st + kPD));
-        const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(ibase + (int64_t)(kt / kPK) * kVTile, kVTile);
+        int8_t *st = kring + (j % kSlots) * kKTile;
 #pragma unroll
-        for (int i = 0; i < S::PER_WAVE; ++i)
+        for (int i = 0; i < kKBlocks; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                i < S::K_LOADS ? kr : vr,
-                (__attribute__((address_space(3))) void *)(st + 1024 * (wave + WAVES * i)), 16,
-                loff[i], 0, 0, 0);
+                kr, (__attribute__((address_space(3))) void *)(st + 1024 * (wave + kWaves * i)), 16,
+                koff[i], 0, 0, 0);
+    };
+    auto issue_v = [&](int j) {  // V image of tile j into V slot j % 3
+        const __amdgpu_buffer_rsrc_t vr =
+            buffer_rsrc(ibase + (int64_t)(kt0 / kPK + j) * kVTile, kVTile);
+        int8_t *st = vring + (j % kSlots) * kVTile;
+#pragma unroll
+        for (int i = 0; i < kVBlocks; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vr, (__attribute__((address_space(3))) void *)(st + 1024 * (wave + kWaves * i)), 16,
+                voff[i], 0, 0, 0);
     };
 
     // LDS operand positions: K row 32u + col, chunk 2t + grp; V row 32d + col, chunk
@@ -273,32 +349,46 @@ __device__ __forceinline__ void packed_tile(const PackedArgs &a, int b, int h, i
     for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int s = 0; s < 2; ++s) vpos[u][s] = col * 128 + 16 * swz(col, 4 * u + 2 * grp + s);
+    const f16x8 ones = row_sum_pattern(lane);
+    const i32x16 bias = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
+                         kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
+                         kScoreBias, kScoreBias, kScoreBias, kScoreBias};
 
-    float m_run = -INFINITY, l_hi = 0.0f, l_lo = 0.0f;
+    float m_run = -INFINITY;
+    f32x4 rs_hi = {}, rs_lo = {};
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
+    auto operand = [](const uint32_t (&w)[4]) {
+        return __builtin_bit_cast(f16x8, i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+    };
 
-    auto tile_math = [&](const int kt, const int8_t *sK, auto mask_tag) {
-        constexpr bool need_mask = decltype(mask_tag)::value;
-        const int8_t *sV = sK + kKTile;
-        i32x16 sc[2];
+    i32x16 sc[2], nx[2];  // scores of the current and of the next tile
+    auto scores = [&](i32x16 (&out)[2], int j) {
+        const int8_t *sK = kring + (j % kSlots) * kKTile;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            sc[u] = i32x16{};
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int t = 0; t < kPD / 32; ++t)
-                sc[u] = mfma_32x32x32_i8(*reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]),
-                                         qop[t], sc[u]);
-        }
-        if constexpr (need_mask) {
+                out[u] = mfma_32x32x32_i8(*reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]),
+                                          qop[t], t == 0 ? (BIAS ? bias : i32x16{}) : out[u]);
+    };
+    // Tile j: masks, the lazy rescale, the probabilities and their row sums, P.V.
+    auto tile_math = [&](const int j, auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        const int kt = kt0 + kPK * j;
+        bool need = false;
+        if constexpr (MASKED) {
+            need = !(kt + kPK - 1 <= full_hi && kt >= full_lo);  // uniform
+            if (need) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kt + 32 * u + 16 * grp + r;
-                    if (key < lo || key > hi) sc[u][r] = INT32_MIN;
-                }
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kt + 32 * u + 16 * grp + r;
+                        if (key < lo || key > hi) sc[u][r] = kMasked;
+                    }
+            }
         }
         int mi = sc[0][0];
 #pragma unroll
@@ -306,115 +396,110 @@ __device__ __forceinline__ void packed_tile(const PackedArgs &a, int b, int h, i
 #pragma unroll
             for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc[u][r]);
         // c > 0, so the largest float score is c times the largest integer.
-        float mt = mi == INT32_MIN ? -INFINITY : (float)mi * c;
+        float mt = mi == kMasked ? -INFINITY : score_float<BIAS>(mi) * c;
         mt = xor32_max(mt);
         if (__any(mt > m_run + kLazy)) {  // wave-uniform
             const float m_new = fmaxf(m_run, mt);
             const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
-            l_hi *= alpha;
-            if (LO) l_lo *= alpha;
+            scale_row_sums(rs_hi, alpha, lane);
+            if (LO) scale_row_sums(rs_lo, alpha, lane);
 #pragma unroll
             for (int d = 0; d < DB; ++d) acc[d] *= alpha;
         }
-        // P in fp16 pairs (4 words per 8 keys) and, with LO, the fp16 residuals.
-        uint32_t phi[2][2][4], plo[2][2][4];
-        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        // Per chunk of 16 keys: the probabilities, their fp16 row sums, then the
+        // products (the residual products of the value blocks that need them right
+        // after, so that a chunk's residuals die with it).
+        const int8_t *sV = vring + (j % kSlots) * kVTile;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int s = 0; s < 2; ++s)
+            for (int s = 0; s < 2; ++s) {
+                uint32_t phi[4], plo[4];
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) {
                     float p[2];
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
                         const int r = 8 * s + e + i;
-                        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[u][r], c, -m_run));
-                        if constexpr (need_mask) {
-                            if (sc[u][r] == INT32_MIN) p[i] = 0.0f;
-                        }
+                        p[i] = __builtin_amdgcn_exp2f(
+                            __builtin_fmaf(score_float<BIAS>(sc[u][r]), c, -m_run));
+                        // a masked key of a row with nothing visible yet (m_run = -inf)
+                        if (MASKED && need && sc[u][r] == kMasked) p[i] = 0.0f;
                     }
-                    const uint32_t h = pack_f16(p[0], p[1]);
-                    phi[u][s][e / 2] = h;
-                    // Row sums of exactly the fp16 values the products use, fp32 accumulation.
-                    l_hi = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, h), one, l_hi, false);
-                    if (LO) {
-                        const uint32_t r = residual_f16(h, p[0], p[1]);
-                        plo[u][s][e / 2] = r;
-                        l_lo = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, r), one, l_lo, false);
-                    }
+                    const uint32_t hw = pack_f16(p[0], p[1]);
+                    phi[e / 2] = hw;
+                    if (LO) plo[e / 2] = residual_f16(hw, p[0], p[1]);
                 }
-        auto operand = [](const uint32_t (&w)[4]) {
-            return __builtin_bit_cast(f16x8, i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
-        };
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
+                rs_hi = mfma_16x16x32_f16(ones, operand(phi), rs_hi);
+                if (LO) rs_lo = mfma_16x16x32_f16(ones, operand(plo), rs_lo);
 #pragma unroll
                 for (int d = 0; d < DB; ++d)
                     acc[d] = mfma_32x32x16_f16(
                         *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[u][s]),
-                        operand(phi[u][s]), acc[d]);
-        if (LO) {
-            // The residual products of the value blocks that need them (uniform).
+                        operand(phi), acc[d]);
+                if (LO) {
 #pragma unroll
-            for (int d = 0; d < DB; ++d) {
-                if ((pmask >> d) & 1) {
-#pragma unroll
-                    for (int u = 0; u < 2; ++u)
-#pragma unroll
-                        for (int s = 0; s < 2; ++s)
+                    for (int d = 0; d < DB; ++d)
+                        if ((pmask >> d) & 1)  // uniform
                             acc[d] = mfma_32x32x16_f16(
                                 *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[u][s]),
-                                operand(plo[u][s]), acc[d]);
+                                operand(plo), acc[d]);
                 }
             }
-        }
     };
 
-    // Each wave has issued PER_WAVE loads per tile; the next tile's may still be in
-    // flight when this tile's must have landed (vmcnt in bits 3:0 and 15:14 of the
-    // s_waitcnt immediate; 0xf70 leaves expcnt and lgkmcnt unconstrained).
-    constexpr int kNext = S::PER_WAVE;
-    static_assert(kNext < 16, "vmcnt fits the low field");
-    issue(0);
-    if (n_tiles > 1) issue(1);
-    // Steps [it_a, it_b): tiles every row of the workgroup sees whole.
+    // Loads: K of tile 0, then per iteration g the group {K(g + 1), V(g)}, issued two
+    // iterations ahead. Iteration j waits for its own group (the next group may be
+    // in flight; counts are this wave's loads, vmcnt in bits 3:0 of the s_waitcnt
+    // immediate, 0xf70 leaving expcnt and lgkmcnt unconstrained) and a barrier makes
+    // every wave's loads visible and frees the slots of tiles j - 1 (values) and j
+    // (keys, read in iteration j - 1).
+    auto group_loads = [&](int g) {
+        return (g + 1 < n_tiles ? kKBlocks : 0) + (g < n_tiles ? kVBlocks : 0);
+    };
+    auto issue_group = [&](int g) {
+        if (g + 1 < n_tiles) issue_k(g + 1);
+        if (g < n_tiles) issue_v(g);
+    };
+    auto wait_loads = [](int n) {  // at most n of this wave's loads still in flight
+        switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(0xf70); break;
+        case kKBlocks: __builtin_amdgcn_s_waitcnt(0xf70 | kKBlocks); break;
+        case kVBlocks: __builtin_amdgcn_s_waitcnt(0xf70 | kVBlocks); break;
+        default: __builtin_amdgcn_s_waitcnt(0xf70 | (kKBlocks + kVBlocks)); break;
+        }
+    };
+    static_assert(kKBlocks + kVBlocks < 16, "vmcnt fits the low field");
+    issue_k(0);
+    issue_group(0);
+    issue_group(1);
+    wait_loads(group_loads(0) + group_loads(1));
+    __builtin_amdgcn_s_barrier();
+    scores(sc, 0);
+    // Tiles [it_a, it_b) are whole for every row of the workgroup: no masks.
     const int wg_full_lo = a.window > 0 ? a.query_start + r_last + 1 - a.window : 0;
     const int wg_full_hi = min(a.query_start + q0, a.kv_len - 1);
     const int it_a = max(0, wg_full_lo - kt0 + kPK - 1) / kPK;
     const int span = wg_full_hi + 1 - kt0;
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kPK : 0));
-    auto step = [&](const int j, auto every_row_tag) {
-        constexpr bool every_row = decltype(every_row_tag)::value;
-        if (j + 1 < n_tiles) __builtin_amdgcn_s_waitcnt(0xf70 | kNext);
-        else __builtin_amdgcn_s_waitcnt(0xf70);
-        // Every wave's loads of tile j are in LDS and every wave is done with tile
-        // j - 1, whose stage tile j + 2 now fills. A bare barrier (no wait for the
-        // loads still in flight).
+    auto step = [&](const int j, auto masked_tag) {
+        wait_loads(group_loads(j + 1));
         __builtin_amdgcn_s_barrier();
-        if (j + 2 < n_tiles) issue(j + 2);
-        const int kt = kt0 + kPK * j;
-        const int8_t *sK = smem + (j % kStages) * kStage;
-        if constexpr (every_row) {
-            tile_math(kt, sK, std::false_type{});
-        } else if (wave_active && kt <= wk_hi && kt + kPK - 1 >= wk_lo) {  // wave-uniform
-            if (kt + kPK - 1 <= full_hi && kt >= full_lo)
-                tile_math(kt, sK, std::false_type{});
-            else
-                tile_math(kt, sK, std::true_type{});
-        }
+        issue_group(j + 2);
+        if (j + 1 < n_tiles) scores(nx, j + 1);  // on the matrix cores beside tile j's softmax
+        tile_math(j, masked_tag);
+        sc[0] = nx[0];
+        sc[1] = nx[1];
     };
     int j = 0;
-    for (; j < it_a; ++j) step(j, std::false_type{});
-    for (; j < it_b; ++j) step(j, std::true_type{});
-    for (; j < n_tiles; ++j) step(j, std::false_type{});
+    for (; j < it_a; ++j) step(j, std::true_type{});
+    for (; j < it_b; ++j) step(j, std::false_type{});
+    for (; j < n_tiles; ++j) step(j, std::true_type{});
 
+    const float lh = row_sum_of_lane(rs_hi, lane);
+    const float ll = LO ? row_sum_of_lane(rs_lo, lane) : 0.0f;
     if (row_ok) {
-        const float lh = xor32_sum(l_hi);
-        const float ll = LO ? xor32_sum(l_lo) : 0.0f;
         float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
@@ -428,21 +513,20 @@ __device__ __forceinline__ void packed_tile(const PackedArgs &a, int b, int h, i
             }
         }
     }
-    // The next tile of this workgroup reuses the stages.
+    // The next tile of this workgroup reuses the rings.
     __syncthreads();
 }
 
 // Blocks of (batch, kv head) whose dequantized values reach above kPreciseAbove:
 // the largest |code| of each 32-channel block over the head's tiles, times the
 // value scale. Uniform over the workgroup.
-template <int WAVES>
 __device__ __forceinline__ uint32_t precise_blocks(const PackedArgs &a, int b, int kvh,
                                                    uint32_t *sRed) {
     if (a.all_precise) return 0xFu;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t *bm = a.bmax + (int64_t)(b * a.kv_heads + kvh) * a.kv_tiles;
     uint32_t m[4] = {0, 0, 0, 0};
-    for (int t = tid; t < a.kv_tiles; t += 64 * WAVES) {
+    for (int t = tid; t < a.kv_tiles; t += 64 * kWaves) {
         const uint32_t w = bm[t];
 #pragma unroll
         for (int i = 0; i < 4; ++i) m[i] = max(m[i], (w >> (8 * i)) & 0xffu);
@@ -455,7 +539,7 @@ __device__ __forceinline__ uint32_t precise_blocks(const PackedArgs &a, int b, i
     }
     __syncthreads();
     uint32_t top[4] = {0, 0, 0, 0};
-    for (int w = 0; w < WAVES; ++w)
+    for (int w = 0; w < kWaves; ++w)
 #pragma unroll
         for (int i = 0; i < 4; ++i) top[i] = max(top[i], sRed[w * 4 + i]);
     __syncthreads();  // sRed is reused by the next item
@@ -467,16 +551,11 @@ __device__ __forceinline__ uint32_t precise_blocks(const PackedArgs &a, int b, i
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)mask);
 }
 
-// Workgroups resident per compute unit: 4-wave workgroups run two at a time (2 x 72 KB
-// of LDS), so the two waves on each SIMD belong to different workgroups and drift
-// apart (one computes scores while the other runs its softmax).
-template <int WAVES>
-constexpr int kPackedPerCu = WAVES == 4 ? 2 : 1;
-
-template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES, kPackedPerCu<WAVES>) void prefill_packed_kernel(PackedArgs a) {
-    __shared__ __attribute__((aligned(1024))) int8_t smem[kStages * kStage];
-    __shared__ uint32_t sRed[4 * WAVES];
+// Two workgroups per compute unit: the two waves on each SIMD belong to different
+// workgroups and fill each other's waits.
+__global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(PackedArgs a) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kKRing + kVRing];
+    __shared__ uint32_t sRed[4 * kWaves];
     const int G = gridDim.x, g = blockIdx.x;
     const int x = g % kXcdCount, per = G / kXcdCount, rem = G % kXcdCount;
     const int L = x * per + min(x, rem) + g / kXcdCount;  // XCD-contiguous logical index
@@ -484,14 +563,27 @@ __global__ __launch_bounds__(64 * WAVES, kPackedPerCu<WAVES>) void prefill_packe
         const int bh = it / a.per_head, i = it % a.per_head;
         const int b = bh / a.q_heads, h = bh % a.q_heads;
         const int kvh = h / (a.q_heads / a.kv_heads);
-        const uint32_t pmask = precise_blocks<WAVES>(a, b, kvh, sRed);
+        const uint32_t pmask = precise_blocks(a, b, kvh, sRed);
         const int light = i, heavy = a.q_tiles - 1 - i;
+        // Scores read as biased floats need the biased maximum's rounding (half an
+        // ulp of 12582912 c) well below the lazy-rescale margin: c <= 4 (any q
+        // scale granularity but per token, where c varies by row).
+        const bool biased =
+            a.q_gran != REEF_SCALE_PER_TOKEN &&
+            scale_at(a.qs, a.q_gran, b, h, 0, a.q_heads, a.q_len) *
+                    scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) * a.score_scale <=
+                4.0f;
+        auto run = [&](auto lo_tag, auto bias_tag) {
+            constexpr bool LO = decltype(lo_tag)::value, BIAS = decltype(bias_tag)::value;
+            packed_tile<LO, BIAS>(a, b, h, light, smem, pmask);
+            if (heavy != light) packed_tile<LO, BIAS>(a, b, h, heavy, smem, pmask);
+        };
         if (pmask) {
-            packed_tile<WAVES, true>(a, b, h, light, smem, pmask);
-            if (heavy != light) packed_tile<WAVES, true>(a, b, h, heavy, smem, pmask);
+            if (biased) run(std::true_type{}, std::true_type{});
+            else run(std::true_type{}, std::false_type{});
         } else {
-            packed_tile<WAVES, false>(a, b, h, light, smem, 0);
-            if (heavy != light) packed_tile<WAVES, false>(a, b, h, heavy, smem, 0);
+            if (biased) run(std::false_type{}, std::true_type{});
+            else run(std::false_type{}, std::false_type{});
         }
     }
 }
@@ -510,7 +602,6 @@ reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *
                                   const int64_t (&vst)[3], const float *q_scales,
                                   const float *k_scales, const float *v_scales, float *out,
                                   const int64_t (&ost)[3], void *image, hipStream_t stream) {
-    constexpr int WAVES = REEF_PACKED_WAVES;
     const int64_t tiles = ceil_div(p->kv_len, kPK);
     const int64_t bkv = p->batch * p->kv_heads;
     if (tiles > 65535 || bkv > 65535) return REEF_UNSUPPORTED;
@@ -557,15 +648,15 @@ reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *
     a.q_gran = p->q_granularity;
     a.kv_gran = p->kv_granularity;
     a.kv_tiles = (int32_t)tiles;
-    a.q_tiles = (int32_t)ceil_div(p->q_len, PackedShape<WAVES>::BM);
+    a.q_tiles = (int32_t)ceil_div(p->q_len, kBM);
     a.per_head = (a.q_tiles + 1) / 2;
     const int64_t items = (int64_t)a.per_head * p->batch * p->q_heads;
     if (items >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
     a.items = (int32_t)items;
     a.all_precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0;
-    const int64_t grid = std::min<int64_t>(items, kPackedPerCu<WAVES> * compute_units());
-    hipLaunchKernelGGL(prefill_packed_kernel<WAVES>, dim3((unsigned)grid), dim3(64 * WAVES), 0,
-                       stream, a);
+    const int64_t grid = std::min<int64_t>(items, kPerCu * compute_units());
+    hipLaunchKernelGGL(prefill_packed_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream,
+                       a);
     return launch_status();
 }
 
