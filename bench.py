@@ -4,16 +4,19 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
 python bench.py --profile-pass   (a few launches of every timed kernel and of a plain
                                   copy of known size, for hardware-counter runs)
 
-Headline (the JSON line's value): causal int8 prefill attention, batch 1, 32
-heads, seq 2048, head_dim 128, per-head scales -- TOPS of algorithmic work
-(4 * head_dim per visible query-key pair) with the int8 inputs resident in HBM.
-One step is one launch of the prefill kernel over the whole batch.
+Headline (the JSON line's value): causal int8 prefill attention, batch 4, 32
+heads, seq 8192, head_dim 128, per-head scales, values with 1% of the channels
+scaled x8 as activation outliers -- TOPS of algorithmic work (4 * head_dim per
+visible query-key pair) with the int8 inputs resident in HBM. One step is one
+call of the prefill entry point over the whole batch.
 
-Also reported in the same line: the int8-KV decode configurations (B64 32q/8kv
-L4096 contiguous; B128 8q/1kv ragged L in [512, 8192] over a 16-token paged
-cache) as GB/s of algorithmic bytes against HBM peak, and the Reef engine's CPU
-path (its own functions, compiled from its headers into oracle/_ref) timed on a
-bounded sample of the headline workload on this host.
+Also reported in the same line: the other prefill workloads (1x32x2048x128 MHA,
+1x8x4096x128 GQA 8:1), the int8-KV decode configurations (B64 32q/8kv L4096
+contiguous; B128 8q/1kv ragged L in [512, 8192] over a 16-token paged cache) as
+GB/s of algorithmic bytes against HBM peak, and the Reef engine's CPU path (its
+own functions, compiled from its headers into oracle/_ref) timed on this host's
+cores: a bounded sample of the headline workload, the whole 1x32x2048x128
+prefill and the whole B64 L4096 decode step.
 """
 from __future__ import annotations
 
@@ -34,21 +37,25 @@ sys.path.insert(0, ROOT)
 METRIC = "prefill int8 attn TOPS (% MFMA peak); decode KV GB/s (% HBM peak)"
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 matrix peak, TOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+CPU_THREADS = 16          # host-core share of one GPU on the benchmark machines
+PREFILL_WORKLOADS = ["prefill_1x1x128x64", "prefill_1x32x2048x128", "prefill_4x32x8192x128",
+                     "prefill_1x8x4096x128_gqa"]
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+    ap.add_argument("--cpu-seconds", type=float, default=16.0,
                     help="approximate budget of the CPU-baseline sample")
-    ap.add_argument("--prefill", default="prefill_1x32x2048x128",
-                    choices=["prefill_1x1x128x64", "prefill_1x32x2048x128",
-                             "prefill_4x32x8192x128", "prefill_1x8x4096x128_gqa"],
-                    help="prefill workload to time (the headline 1x32x2048x128 by default)")
+    ap.add_argument("--prefill", default="prefill_4x32x8192x128",
+                    choices=PREFILL_WORKLOADS,
+                    help="headline prefill workload (4x32x8192x128 by default)")
+    ap.add_argument("--prefill-other", default="prefill_1x32x2048x128,prefill_1x8x4096x128_gqa",
+                    help="further prefill workloads reported beside the headline (comma list)")
     ap.add_argument("--decode", default="decode_b64_l4096,decode_paged_b128_ragged",
                     help="decode workloads to time (comma list of decode_b64_l4096, "
                          "decode_paged_b128_ragged)")
@@ -187,20 +194,38 @@ def prefill_setup(torch, reef, W, name):
     return cfg, (qf, kf, vf), (q, k, v, qs, ks, vs), out, launch
 
 
-def bench_prefill(torch, reef, W, args):
-    cfg, (qf, kf, vf), (q, k, v, qs, ks, vs), out, launch = prefill_setup(
-        torch, reef, W, args.prefill)
+def prefill_kernels(torch, cfg):
+    """The kernels the entry point's automatic schedule launches for `cfg`: the packed
+    schedule (a V-image pack, then the attention kernel) when head_dim is 128, the
+    scales are not per token and there is at least one pair of 256-row query tiles
+    per compute unit; the one-item kernel otherwise."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    pairs = ((cfg.seq + 255) // 256 + 1) // 2 * cfg.batch * cfg.q_heads
+    if cfg.head_dim == 128 and pairs >= cus:
+        return "vt_pack_kernel + prefill_packed_kernel"
+    return "prefill_kernel"
 
-    quant = quant_launcher(torch, reef, cfg, (qf, kf, vf))
-    quant_ms, quant_how = quant_graph_ms(torch, quant)
-    quant.check()
-    del qf, kf, vf, quant
-    wall_ms, kern_ms = timed(torch, launch, args.steps, args.warmup)
+
+def bench_prefill(torch, reef, W, name, steps, warmup, with_quant=True):
+    cfg, (qf, kf, vf), (q, k, v, qs, ks, vs), out, launch = prefill_setup(torch, reef, W, name)
+    quant = None
+    if with_quant:
+        ql = quant_launcher(torch, reef, cfg, (qf, kf, vf))
+        quant_ms, quant_how = quant_graph_ms(torch, ql)
+        ql.check()
+        quant_bytes = ((q.numel() + k.numel() + v.numel()) * 5
+                       + 4 * (qs.numel() + ks.numel() + vs.numel()))
+        quant = {"kernels": "per-head quantize of q, k and v (per tensor: block maxima, "
+                            "then scales and quantize)",
+                 "timing": quant_how, "ms": round(quant_ms, 4),
+                 "GB/s": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1)}
+        del ql
+    del qf, kf, vf
+    wall_ms, kern_ms = timed(torch, launch, steps, warmup)
     if not torch.isfinite(out).all():
         raise RuntimeError("prefill produced non-finite output")
-    ops = cfg.algorithmic_ops()
-    quant_bytes = (q.numel() + k.numel() + v.numel()) * 5 + 4 * (qs.numel() + ks.numel() + vs.numel())
-    return cfg, ops, wall_ms, kern_ms, (quant_ms, quant_how), quant_bytes, (q, k, v, qs, ks, vs)
+    del out
+    return cfg, cfg.algorithmic_ops(), wall_ms, kern_ms, quant, (q, k, v, qs, ks, vs)
 
 
 def decode_query(torch, reef, cfg, g):
@@ -427,41 +452,165 @@ def recorded_traffic(workload):
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(cfg, inputs, budget_s):
-    """The engine's own CPU attention (oracle/_ref, kind "reference") or, when it was
-    not built, the oracle restatement (kind "port"): one thread, whole heads of the
-    headline workload until the time budget is spent; ops per second are scaled
-    from the heads done."""
-    import oracle
-    q, k, v, qs, ks, vs = (t.cpu().numpy() for t in inputs)
-    S, D = cfg.seq, cfg.head_dim
-    kind = "reference" if oracle.ref_available() else "port"
-    heads, t_total = 0, 0.0
-    while t_total < budget_s and heads < cfg.q_heads:
-        h = heads
-        t0 = time.perf_counter()
-        if kind == "reference":
-            oracle.ref_attention_int8_head(q[0, h], k[0, h], v[0, h], np.full(S, qs[h], np.float32),
-                                           np.full(S, ks[h], np.float32),
-                                           np.full(S, vs[h], np.float32), 0, 0, cfg.softmax_scale)
-        else:
-            p = oracle.Problem(1, 1, 1, S, S, D, softmax_scale=cfg.softmax_scale)
-            oracle.attention_int8(p, q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], qs[h:h + 1],
-                                  ks[h:h + 1], vs[h:h + 1], threads=1)
-        t_total += time.perf_counter() - t0
-        heads += 1
-    ops = 4 * D * heads * S * (S + 1) // 2
-    tops = ops / t_total / 1e12
-    cpu_model = ""
+def host_cpu():
+    """(CPU model name, logical CPUs this process may run on)."""
+    model = ""
     try:
         with open("/proc/cpuinfo") as f:
-            cpu_model = next((l.split(":", 1)[1].strip() for l in f if "model name" in l), "")
+            model = next((l.split(":", 1)[1].strip() for l in f if "model name" in l), "")
     except OSError:
         pass
-    return {"value": tops, "unit": "TOPS", "cores": 1, "kind": kind,
-            "sample": f"{heads} of {cfg.q_heads} heads of the headline workload "
-                      f"({t_total:.1f} s, 1 thread, {os.cpu_count()} host cores, {cpu_model})",
-            "seconds_full_workload_extrapolated": t_total * cfg.q_heads / heads}
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return model, n
+
+
+def causal_pairs(r0, rows):
+    """Visible query-key pairs of query rows [r0, r0 + rows) of a causal head whose
+    first query is key 0 (row i sees keys 0..i)."""
+    return rows * (2 * r0 + rows + 1) // 2
+
+
+def cpu_prefill_rows(oracle, kind, cfg, host, b, h, r0, rows):
+    """Query rows [r0, r0 + rows) of head (b, h) through the CPU path (the engine
+    computes every key of every row it is given and masks; the oracle skips the
+    invisible ones). Returns the algorithmic ops of those rows."""
+    q, k, v, qs, ks, vs = host
+    S, D = cfg.seq, cfg.head_dim
+    kvh = h // (cfg.q_heads // cfg.kv_heads)
+    if kind == "reference":
+        oracle.ref_attention_int8_head(q[b, h, r0:r0 + rows], k[b, kvh], v[b, kvh],
+                                       np.full(rows, qs[h], np.float32),
+                                       np.full(S, ks[kvh], np.float32),
+                                       np.full(S, vs[kvh], np.float32), r0, 0, cfg.softmax_scale)
+    else:
+        p = oracle.Problem(1, 1, 1, rows, S, D, query_start=r0, softmax_scale=cfg.softmax_scale)
+        oracle.attention_int8(p, q[b:b + 1, h:h + 1, r0:r0 + rows], k[b:b + 1, kvh:kvh + 1],
+                              v[b:b + 1, kvh:kvh + 1], qs[h:h + 1], ks[kvh:kvh + 1],
+                              vs[kvh:kvh + 1], threads=1)
+    return 4 * D * causal_pairs(r0, rows)
+
+
+def run_jobs(jobs, threads):
+    """Runs the callables on `threads` threads (the CPU path is a C call that releases
+    the interpreter lock); returns (sum of their results, wall seconds)."""
+    from concurrent.futures import ThreadPoolExecutor
+    t0 = time.perf_counter()
+    if threads == 1:
+        total = sum(j() for j in jobs)
+    else:
+        with ThreadPoolExecutor(threads) as ex:
+            total = sum(ex.map(lambda j: j(), jobs))
+    return total, time.perf_counter() - t0
+
+
+def cpu_prefill_sample(oracle, kind, cfg, host, threads, budget_s):
+    """A bounded sample of a prefill workload: first one thread on one slice of query
+    rows, sized from a short probe to about a quarter of the budget; then `threads`
+    slices at once, on different heads, at offsets spread evenly over the causal
+    range, sized to about half of it. Returns the record of both."""
+    S, H, B = cfg.seq, cfg.q_heads, cfg.batch
+    probe_rows = min(S, 32)
+    ops, t = run_jobs([lambda: cpu_prefill_rows(oracle, kind, cfg, host, 0, 0, S - probe_rows,
+                                                probe_rows)], 1)
+    per_row = t / probe_rows  # the engine's time per row does not depend on the row
+    rows1 = int(max(1, min(S, budget_s * 0.25 / per_row)))
+    ops1, t1 = run_jobs([lambda: cpu_prefill_rows(oracle, kind, cfg, host, 0, 0, S - rows1,
+                                                  rows1)], 1)
+    rows = int(max(1, min(S, budget_s * 0.5 / per_row)))
+    jobs = []
+    for i in range(threads):
+        head = (i * 7) % (B * H)
+        r0 = min(S - rows, (S * i) // threads)
+        jobs.append(lambda b=head // H, h=head % H, r0=r0: cpu_prefill_rows(
+            oracle, kind, cfg, host, b, h, r0, rows))
+    opsn, tn = run_jobs(jobs, threads)
+    value = opsn / tn / 1e12
+    return {
+        "value": value, "unit": "TOPS", "cores": threads, "kind": kind,
+        "sample": f"{threads} slices of {rows} query rows (of {S}) of {cfg.name}, one per "
+                  f"thread on {threads} threads, offsets spread over the causal range "
+                  f"({tn:.1f} s); ops are the algorithmic ops of the rows done",
+        "single_thread": {"value": ops1 / t1 / 1e12, "unit": "TOPS", "cores": 1,
+                          "sample": f"the last {rows1} query rows of one head ({t1:.1f} s)"},
+        "seconds_full_workload_extrapolated": tn * (S * B * H) / (rows * threads),
+        "extrapolated_from": "the sample's wall time per row, scaled to every row of every "
+                             "head at the same thread count",
+    }
+
+
+def cpu_prefill_full(oracle, kind, cfg, host, threads):
+    """Every head of a prefill workload, one job per head on `threads` threads."""
+    jobs = [lambda b=b, h=h: cpu_prefill_rows(oracle, kind, cfg, host, b, h, 0, cfg.seq)
+            for b in range(cfg.batch) for h in range(cfg.q_heads)]
+    ops, t = run_jobs(jobs, threads)
+    return {"workload": cfg.name, "value": ops / t / 1e12, "unit": "TOPS", "seconds": t,
+            "cores": threads, "kind": kind, "sample": "the whole workload"}
+
+
+def cpu_decode_full(oracle, kind, cfg, host, threads):
+    """Every (sequence, query head) of a contiguous decode step through the CPU path:
+    one query row at position L - 1 over the L cached keys of its KV head, per-token
+    K/V scales, one scale per query head. GB/s of the step's algorithmic bytes."""
+    q, qsc, k, v, ksc, vsc = host
+    B, Hq, Hkv, D, L = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.context
+    scale = 1.0 / math.sqrt(D)
+
+    def job(b):
+        for h in range(Hq):
+            kvh = h // (Hq // Hkv)
+            if kind == "reference":
+                oracle.ref_attention_int8_head(q[b, h][None], k[b, kvh], v[b, kvh],
+                                               np.full(1, qsc[h], np.float32), ksc[b, kvh],
+                                               vsc[b, kvh], L - 1, 0, scale)
+            else:
+                p = oracle.Problem(1, 1, 1, 1, L, D, query_start=L - 1, softmax_scale=scale,
+                                   q_granularity=oracle.GRAN_HEAD,
+                                   kv_granularity=oracle.GRAN_TOKEN)
+                oracle.attention_int8(p, q[b, h][None, None, None], k[b, kvh][None, None],
+                                      v[b, kvh][None, None], qsc[h:h + 1], ksc[b, kvh],
+                                      vsc[b, kvh], threads=1)
+        return 0
+    _, t = run_jobs([lambda b=b: job(b) for b in range(B)], threads)
+    nbytes = cfg.kv_bytes()
+    return {"workload": cfg.name, "value": nbytes / t / 1e9, "unit": "GB/s", "seconds": t,
+            "cores": threads, "kind": kind, "sample": "the whole decode step"}
+
+
+def cpu_baselines(torch, reef, W, cfg, inputs, budget_s):
+    """The CPU path on this host: a bounded sample of the headline prefill (the
+    record's value), plus the whole 1x32x2048x128 prefill and the whole B64 L4096
+    decode step on the same threads."""
+    import oracle
+    kind = "reference" if oracle.ref_available() else "port"
+    model, ncpu = host_cpu()
+    threads = max(1, min(CPU_THREADS, ncpu))
+    host = tuple(t.cpu().numpy() for t in inputs)
+    rec = cpu_prefill_sample(oracle, kind, cfg, host, threads, budget_s)
+    rec["host"] = {"cpu_model": model, "logical_cpus": ncpu, "threads_used": threads}
+    full = []
+    c2, _, t2, _, _ = prefill_setup(torch, reef, W, "prefill_1x32x2048x128")
+    full.append(cpu_prefill_full(oracle, kind, c2, tuple(t.cpu().numpy() for t in t2), threads))
+    del t2
+    c3, _, (q, qsc, k, vp, ksc, vsc, _) = decode_contiguous_setup(torch, reef, W)
+    B, Hkv, D, L = c3.batch, c3.kv_heads, c3.head_dim, c3.context
+    v_tok = vp.view(B, Hkv, L // 16, D, 16).transpose(3, 4).reshape(B, Hkv, L, D)
+    host3 = (q.cpu().numpy(), qsc.cpu().numpy(), k.cpu().numpy(), v_tok.cpu().numpy(),
+             ksc.cpu().numpy(), vsc.cpu().numpy())
+    del q, qsc, k, vp, ksc, vsc, v_tok
+    torch.cuda.empty_cache()
+    full.append(cpu_decode_full(oracle, kind, c3, host3, threads))
+    rec["full_runs"] = full
+    return rec
+
+
+def prefill_record(torch, cfg, ops, wall_ms, kern_ms):
+    return {"workload": cfg.name, "kernels": prefill_kernels(torch, cfg),
+            "ms_per_step": round(wall_ms, 5), "kernel_ms": round(kern_ms, 5),
+            "TOPS": round(ops / (kern_ms * 1e-3) / 1e12, 2),
+            "frac_int8_peak": round(ops / (kern_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
 
 
 def main():
@@ -476,10 +625,15 @@ def main():
     from reef_amd import workloads as W
 
     reef.lib()
+    others = [n for n in args.prefill_other.split(",") if n and n != args.prefill]
+    for n in others:
+        if n not in PREFILL_WORKLOADS:
+            raise SystemExit(f"unknown prefill workload {n}")
     if args.profile_pass:
         copy_calibration(torch)
-        args.steps, args.warmup = 3, 1
-        bench_prefill(torch, reef, W, args)
+        for n in [args.prefill] + others:
+            bench_prefill(torch, reef, W, n, 3, 1, with_quant=n == args.prefill)
+            torch.cuda.empty_cache()
         fns = {"decode_b64_l4096": decode_contiguous, "decode_paged_b128_ragged": decode_paged_ragged}
         for fn in (fns[n] for n in args.decode.split(",") if n):
             fn(torch, reef, W, 3, 1)
@@ -488,10 +642,13 @@ def main():
         print(json.dumps({"profile_pass": True, "copy_bytes": COPY_BYTES,
                           "copy_launches": COPY_LAUNCHES}), flush=True)
         return
-    cfg, ops, wall_ms, kern_ms, (quant_ms, quant_how), quant_bytes, inputs = bench_prefill(
-        torch, reef, W, args)
+    cfg, ops, wall_ms, kern_ms, quant, inputs = bench_prefill(
+        torch, reef, W, args.prefill, args.steps, args.warmup)
+    torch.cuda.empty_cache()
     value = ops / (wall_ms * 1e-3) / 1e12
     achieved = ops / (kern_ms * 1e-3) / 1e12
+    outliers = (f", {cfg.outlier_fraction:.0%} of channels x{cfg.outlier_gain:g}"
+                if cfg.outlier_fraction else "")
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -504,22 +661,27 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic: N(0,1) fp32 drawn on the GPU from a fixed seed, quantized per head "
-                "to int8 by the library before timing",
+        "data": "synthetic: N(0,1) fp32 drawn on the GPU from a fixed seed" + outliers +
+                ", quantized per head to int8 by the library before timing",
         "config": {"workload": cfg.name, "batch": cfg.batch, "q_heads": cfg.q_heads,
                    "kv_heads": cfg.kv_heads, "seq_len": cfg.seq, "head_dim": cfg.head_dim,
                    "causal": True, "scales": "per-head"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
                      "traffic": recorded_traffic(args.prefill),
-                     "kernel": "prefill_kernel<128, false, false>",
-                     "kernel_ms": round(kern_ms, 5), "algorithmic_ops_per_launch": ops},
-        "quantize": {"kernels": "per-head quantize of q, k and v (per tensor: block maxima, "
-                                "then scales and quantize)",
-                     "timing": quant_how,
-                     "ms": round(quant_ms, 4),
-                     "GB/s": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1)},
+                     "kernel": prefill_kernels(torch, cfg),
+                     "kernel_ms": round(kern_ms, 5), "algorithmic_ops_per_launch": ops,
+                     "timing": "HIP events on the launch stream around the timed launches; "
+                               "kernel_ms covers every kernel of one entry-point call"},
+        "quantize": quant,
     }
+    other = []
+    for n in others:
+        ocfg, oops, ow, ok, _, _ = bench_prefill(torch, reef, W, n, args.steps, args.warmup,
+                                                 with_quant=False)
+        other.append(prefill_record(torch, ocfg, oops, ow, ok))
+        torch.cuda.empty_cache()
+    rec["prefill_other"] = other
     if not args.no_decode:
         dec = []
         fns = {"decode_b64_l4096": decode_contiguous, "decode_paged_b128_ragged": decode_paged_ragged}
@@ -536,7 +698,7 @@ def main():
         rec["extra"] = bench_extras(torch, reef, W, max(10, args.steps // 2))
         torch.cuda.empty_cache()
     if not args.no_cpu:
-        rec["cpu_baseline"] = cpu_baseline(cfg, inputs, args.cpu_seconds)
+        rec["cpu_baseline"] = cpu_baselines(torch, reef, W, cfg, inputs, args.cpu_seconds)
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)
