@@ -363,18 +363,22 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         return __builtin_bit_cast(f16x8, i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
     };
 
-    i32x16 sc[2], nx[2];  // scores of the current and of the next tile
-    auto scores = [&](i32x16 (&out)[2], int j) {
+    struct Scores {
+        i32x16 u[2];
+    };
+    auto scores = [&](int j) {  // scores of tile j, keys 32u .. 32u + 31 in u[u]
         const int8_t *sK = kring + (j % kSlots) * kKTile;
+        Scores out;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int t = 0; t < kPD / 32; ++t)
-                out[u] = mfma_32x32x32_i8(*reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]),
-                                          qop[t], t == 0 ? (BIAS ? bias : i32x16{}) : out[u]);
+                out.u[u] = mfma_32x32x32_i8(*reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]),
+                                            qop[t], t == 0 ? (BIAS ? bias : i32x16{}) : out.u[u]);
+        return out;
     };
     // Tile j: masks, the lazy rescale, the probabilities and their row sums, P.V.
-    auto tile_math = [&](const int j, auto masked_tag) {
+    auto tile_math = [&](const int j, auto masked_tag, Scores sc) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int kt = kt0 + kPK * j;
         bool need = false;
@@ -386,15 +390,15 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int key = kt + 32 * u + 16 * grp + r;
-                        if (key < lo || key > hi) sc[u][r] = kMasked;
+                        if (key < lo || key > hi) sc.u[u][r] = kMasked;
                     }
             }
         }
-        int mi = sc[0][0];
+        int mi = sc.u[0][0];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc[u][r]);
+            for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc.u[u][r]);
         // c > 0, so the largest float score is c times the largest integer.
         float mt = mi == kMasked ? -INFINITY : score_float<BIAS>(mi) * c;
         mt = xor32_max(mt);
@@ -423,9 +427,9 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
                     for (int i = 0; i < 2; ++i) {
                         const int r = 8 * s + e + i;
                         p[i] = __builtin_amdgcn_exp2f(
-                            __builtin_fmaf(score_float<BIAS>(sc[u][r]), c, -m_run));
+                            __builtin_fmaf(score_float<BIAS>(sc.u[u][r]), c, -m_run));
                         // a masked key of a row with nothing visible yet (m_run = -inf)
-                        if (MASKED && need && sc[u][r] == kMasked) p[i] = 0.0f;
+                        if (MASKED && need && sc.u[u][r] == kMasked) p[i] = 0.0f;
                     }
                     const uint32_t hw = pack_f16(p[0], p[1]);
                     phi[e / 2] = hw;
@@ -476,26 +480,40 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     issue_group(1);
     wait_loads(group_loads(0) + group_loads(1));
     __builtin_amdgcn_s_barrier();
-    scores(sc, 0);
+    Scores sc = scores(0);
     // Tiles [it_a, it_b) are whole for every row of the workgroup: no masks.
     const int wg_full_lo = a.window > 0 ? a.query_start + r_last + 1 - a.window : 0;
     const int wg_full_hi = min(a.query_start + q0, a.kv_len - 1);
     const int it_a = max(0, wg_full_lo - kt0 + kPK - 1) / kPK;
     const int span = wg_full_hi + 1 - kt0;
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kPK : 0));
-    auto step = [&](const int j, auto masked_tag) {
+    // Tile j's softmax and products with the scores of tile j + 1 issued first; returns
+    // those scores.
+    auto step = [&](const int j, auto masked_tag, const Scores &cur) {
         wait_loads(group_loads(j + 1));
         __builtin_amdgcn_s_barrier();
         issue_group(j + 2);
-        if (j + 1 < n_tiles) scores(nx, j + 1);  // on the matrix cores beside tile j's softmax
-        tile_math(j, masked_tag);
-        sc[0] = nx[0];
-        sc[1] = nx[1];
+        Scores next{};
+        if (j + 1 < n_tiles) next = scores(j + 1);  // on the matrix cores beside the softmax
+        tile_math(j, masked_tag, cur);
+        return next;
     };
+    // Two tiles per iteration: the loop-carried scores come back in the registers
+    // they left, with no copies.
     int j = 0;
-    for (; j < it_a; ++j) step(j, std::true_type{});
-    for (; j < it_b; ++j) step(j, std::false_type{});
-    for (; j < n_tiles; ++j) step(j, std::true_type{});
+    auto run = [&](const int end, auto masked_tag) {
+        for (; j + 1 < end; j += 2) {
+            const Scores mid = step(j, masked_tag, sc);
+            sc = step(j + 1, masked_tag, mid);
+        }
+        if (j < end) {
+            sc = step(j, masked_tag, sc);
+            ++j;
+        }
+    };
+    run(it_a, std::true_type{});
+    run(it_b, std::false_type{});
+    run(n_tiles, std::true_type{});
 
     const float lh = row_sum_of_lane(rs_hi, lane);
     const float ll = LO ? row_sum_of_lane(rs_lo, lane) : 0.0f;
