@@ -247,16 +247,20 @@ typedef struct reef_decode_params {
     int64_t window;       /* 0: global */
     float softmax_scale;
     int32_t q_granularity;
-    int32_t num_splits;   /* key-range splits per sequence; 0: library choice */
+    int32_t num_splits;   /* 0: library choice; n > 0: about n waves per (sequence,
+                             kv head) on average (ceil(B * Hkv * n / 4) workgroups) */
     uint32_t flags;
 } reef_decode_params;
 
-/* Bytes of device workspace the decode entry points need for params: one
- * counter per (sequence, kv head) and, when a sequence's keys are split over
- * more than one workgroup, one partial result per workgroup, merged by the last
- * workgroup of the sequence inside the same launch. The workspace must be
- * zero-filled before its first use; every call leaves it ready for the next
- * (no refill). Calls that may run at the same time need separate workspaces. */
+/* Bytes of device workspace the decode entry points need for params. The launch
+ * deals the keys of all (sequence, kv head) items out to its workgroups in equal
+ * runs of 64-key blocks, whatever the context lengths (with at most 2048 items;
+ * beyond that, in equal runs of whole items). The workspace holds one counter per
+ * item and two partial-result slots per workgroup; an item whose keys span several
+ * workgroups is merged by the last of them inside the same launch. The workspace
+ * must be zero-filled before its first use; every call leaves it ready for the
+ * next (no refill). Calls that may run at the same time need separate
+ * workspaces. */
 size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p);
 
 reef_status reef_attention_decode_int8(const reef_decode_params *p, const int8_t *q,
@@ -276,7 +280,7 @@ reef_status reef_attention_decode_int8_paged(
 /* Allocation-free form of reef_attention_decode_int8_paged, with no counterpart in
  * the reference: for callers that cannot allocate or pass device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
- * split-merge workspace is a fixed 8 MiB array inside the library, one per GPU,
+ * split-merge workspace is a fixed 16 MiB array inside the library, one per GPU,
  * held until the process ends; a call whose workspace
  * (reef_attention_decode_workspace_bytes) would exceed it returns REEF_UNSUPPORTED
  * before any launch. Each call clears the counters it uses with a small fill

@@ -30,9 +30,11 @@
 namespace reef {
 namespace {
 
-constexpr int kDecodeWaves = 4;          // waves per workgroup, one split each
+constexpr int kDecodeWaves = 4;          // waves per workgroup
 constexpr int kBlockKeys = 64;           // keys per inner step (4 pages)
 constexpr int kPage = 16;                // tokens per page
+constexpr int kPlanItems = 2048;         // items whose block offsets a workgroup plans in LDS
+constexpr int kWgPerCu = 2;              // resident workgroups per compute unit
 
 struct DecodeArgs {
     const int8_t *q;
@@ -46,8 +48,10 @@ struct DecodeArgs {
     float *slots;           // [B * Hkv, groups] parts (DecodeSlot), with groups > 1
     uint32_t *status;
     int32_t batch, q_heads, kv_heads, group;
-    int32_t max_context, window, splits;
-    int32_t groups;  // partials per (sequence, head): one per workgroup of 4 splits
+    int32_t max_context, window;
+    int32_t items;  // batch * kv_heads: one (sequence, kv head) each
+    int32_t wgs;    // workgroups of the launch
+    int32_t flat;   // 1: the launch's keys are dealt out by 64-key blocks, 0: by items
     int32_t max_blocks, num_pages;               // paged only
     int32_t q_gran;
     float score_scale;  // softmax_scale * log2(e)
@@ -319,7 +323,10 @@ __device__ __forceinline__ float load_query(const DecodeArgs &a, int b, int head
 
 // Keys [k_begin, k_end) of (sequence b, kv head kvh) in steps of k_step, the next
 // block's loads (and the table entries of the one after) issued before the
-// current block is computed.
+// current block is computed. The first block is loaded into `nxt` and copied,
+// like every later one: the current block's registers are then always written
+// by copies, never by loads still in flight, so computing it waits for nothing
+// the next block's loads are doing.
 template <int D, bool PAGED>
 __device__ __forceinline__ void run_keys(const DecodeArgs &a, int b, int kvh, int lo, int k_begin,
                                          int k_end, int k_step, int n_pages,
@@ -327,10 +334,12 @@ __device__ __forceinline__ void run_keys(const DecodeArgs &a, int b, int kvh, in
                                          DecodeRun<D> &st, bool &bad_page) {
     const int col = lane & 15, grp = lane >> 4;
     DecodeBlock<D> cur, nxt;
-    if (k_begin < k_end)
+    if (k_begin < k_end) {
         load_block<D, PAGED>(a, b, kvh, k_begin, n_pages,
-                             fetch_pages<PAGED>(a, b, k_begin, n_pages, lane), col, grp, cur,
+                             fetch_pages<PAGED>(a, b, k_begin, n_pages, lane), col, grp, nxt,
                              bad_page);
+        cur = nxt;
+    }
     int pg_next = fetch_pages<PAGED>(a, b, k_begin + k_step, n_pages, lane);
     for (int kb = k_begin; kb < k_end; kb += k_step) {
         const bool more = kb + k_step < k_end;
@@ -342,180 +351,301 @@ __device__ __forceinline__ void run_keys(const DecodeArgs &a, int b, int kvh, in
     }
 }
 
-template <int D, bool PAGED>
-__global__ __launch_bounds__(kDecodeWaves * 64, 2) void decode_kernel(DecodeArgs a, float *out) {
-    constexpr int DB = D / 16;   // 16-wide output blocks
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int col = lane & 15, grp = lane >> 4;
-    const int split = blockIdx.x * kDecodeWaves + wave;
-    const int kvh = blockIdx.y, b = blockIdx.z;
-    // Every wave reaches the workgroup merge below, so none returns early; a wave
-    // past the last split, or whose split holds no keys, contributes nothing.
-    const bool in_range = split < a.splits;
+// Keys of one item (sequence b = item / kv_heads): its length (0 if the length is
+// out of range), the first visible key, and its 64-key blocks from the block that
+// holds that key. An item with no keys still counts one block, so that some
+// workgroup stores its (zero) output.
+struct ItemKeys {
+    int len, lo, first_block, blocks;
+    bool bad;
+};
 
-    const int head = kvh * a.group + col;   // this lane's query head (live if col < group)
-    const bool head_ok = col < a.group;
-
+__device__ __forceinline__ ItemKeys item_keys(const DecodeArgs &a, int item) {
+    ItemKeys r;
+    const int b = item / a.kv_heads;
     int len = a.context_lens ? a.context_lens[b] : a.max_context;
-    if (len < 1 || len > a.max_context) {
-        if (split == 0 && lane == 0) flag_status(a.status, REEF_STATUS_BIT_BAD_LENGTH);
-        len = 0;
-    }
-    const int lo = a.window > 0 ? max(0, len - a.window) : 0;
-    // Split s takes the 64-key blocks first + s, first + s + splits, ...: at any
-    // moment the splits of a sequence read neighbouring blocks, which keeps the
-    // DRAM accesses of the waves running together close.
-    const int k_step = a.splits * kBlockKeys;
-    const int k_begin = (lo / kBlockKeys + split) * kBlockKeys;
-    const int k_end = in_range ? len : 0;
-    const int n_pages = (len + kPage - 1) / kPage;
+    r.bad = len < 1 || len > a.max_context;
+    if (r.bad) len = 0;
+    r.len = len;
+    r.lo = a.window > 0 ? max(0, len - a.window) : 0;
+    r.first_block = r.lo / kBlockKeys;
+    r.blocks = len > 0 ? (len + kBlockKeys - 1) / kBlockKeys - r.first_block : 1;
+    return r;
+}
 
-    i32x4 qop[D / 64];
-    const float c = load_query<D>(a, b, head, head_ok, grp, qop);
-    DecodeRun<D> st;
-    reset_run<D>(st);
-    bool bad_page = false;
-    run_keys<D, PAGED>(a, b, kvh, lo, k_begin, k_end, k_step, n_pages, qop, c, lane, st, bad_page);
-    float m_run = st.m_run, l_run = st.l_run, s_run = st.s_run;
-    f32x4 acc[DB];
+// sOff[i] = blocks of items 0 .. i-1, for i <= items (a workgroup-wide scan).
+__device__ void plan_blocks(const DecodeArgs &a, int32_t *sOff, int32_t *sWave) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) sOff[0] = 0;
+    int32_t run = 0;
+    for (int base = 0; base < a.items; base += 64 * kDecodeWaves) {
+        const int i = base + tid;
+        int32_t x = i < a.items ? item_keys(a, i).blocks : 0;
 #pragma unroll
-    for (int d = 0; d < DB; ++d) acc[d] = st.acc[d];
-    if (bad_page) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
-
-    // Row sums: this lane holds head col's partial over its 16 keys per block.
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
-
-    // The workgroup's 4 splits merge in LDS (log-sum-exp) into one part. Waves 1..3
-    // hand over (max, sum, accumulator in value units) in a lane-linear layout;
-    // wave 0 merges.
-    __shared__ f32x4 sO[kDecodeWaves - 1][DB][kWave];
-    __shared__ float2 sML[kDecodeWaves - 1][kWave];
-    if (wave > 0) {
-#pragma unroll
-        for (int d = 0; d < DB; ++d) sO[wave - 1][d][lane] = acc[d] * s_run;
-        sML[wave - 1][lane] = float2{m_run, l_run};
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) sWave[wave] = x;
+        __syncthreads();
+        int32_t before = run;
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            if (w < wave) before += sWave[w];
+            run += sWave[w];
+        }
+        if (i < a.items) sOff[i + 1] = before + x;
+        __syncthreads();
     }
+}
+
+// Workgroup g of G owns units [start(g), start(g + 1)) of the T units (64-key
+// blocks of all items, or items), start(g) = g T / G; unit u lies in workgroup
+// ((u + 1) G - 1) / T.
+__device__ __forceinline__ int64_t wg_start(int64_t g, int64_t T, int64_t G) { return g * T / G; }
+__device__ __forceinline__ int wg_of(int64_t u, int64_t T, int64_t G) {
+    return (int)(((u + 1) * G - 1) / T);
+}
+
+// Log-sum-exp merge of the waves' (max, sum, output in absolute value units)
+// through LDS, in wave order; the result is valid in wave 0. The caller places a
+// barrier between this and the next use of sO / sML.
+template <int D>
+__device__ __forceinline__ void merge_waves(float &m, float &l, f32x4 (&o)[D / 16],
+                                            f32x4 (*sO)[D / 16][kWave], float2 *sML, int wave,
+                                            int lane) {
+    constexpr int DB = D / 16;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) sO[wave][d][lane] = o[d];
+    sML[wave * kWave + lane] = float2{m, l};
     __syncthreads();
-    if (wave > 0) return;
+    if (wave != 0) return;
     float mw[kDecodeWaves], lw[kDecodeWaves];
-    mw[0] = m_run;
-    lw[0] = l_run;
 #pragma unroll
-    for (int w = 1; w < kDecodeWaves; ++w) {
-        const float2 x = sML[w - 1][lane];
+    for (int w = 0; w < kDecodeWaves; ++w) {
+        const float2 x = sML[w * kWave + lane];
         mw[w] = x.x;
         lw[w] = x.y;
     }
-    float m = mw[0];
+    float mt = mw[0];
 #pragma unroll
-    for (int w = 1; w < kDecodeWaves; ++w) m = fmaxf(m, mw[w]);
-    float e[kDecodeWaves], l = 0.0f;
+    for (int w = 1; w < kDecodeWaves; ++w) mt = fmaxf(mt, mw[w]);
+    float lt = 0.0f;
+    f32x4 ot[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) ot[d] = f32x4{};
 #pragma unroll
     for (int w = 0; w < kDecodeWaves; ++w) {
-        e[w] = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - m);
-        l += lw[w] * e[w];
-    }
-    // acc[d][i] is (channel 16 d + 4 grp + i, head col): this part's output in
-    // absolute value units.
-    f32x4 o[DB];
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-        o[d] = acc[d] * (s_run * e[0]);
-#pragma unroll
-        for (int w = 1; w < kDecodeWaves; ++w) o[d] += sO[w - 1][d][lane] * e[w];
-    }
-
-    // With more than one workgroup per (sequence, kv head), every part writes
-    // (max, sum, output) to its workspace slot with device-coherent atomic stores,
-    // releases them at agent scope and counts itself in on the item's counter (an
-    // acquire-release increment); the last part acquires at agent scope, merges
-    // the slots in part order (its own from registers, explicit fused
-    // multiply-adds: the same result whichever part finishes last), stores the
-    // output and resets the counter. No second kernel combines splits.
-    const int parts = a.groups;
-    bool store = parts == 1;
-    if (parts > 1) {
-        const int item = b * a.kv_heads + kvh;
-        const int self = blockIdx.x;
-        uint64_t *slots = reinterpret_cast<uint64_t *>(a.slots) +
-                          (int64_t)item * parts * DecodeSlot<D>::ELEMS;
-        uint64_t *so = slots + (int64_t)self * DecodeSlot<D>::ELEMS;
-        auto pack = [](float x0, float x1) {
-            return (uint64_t)__float_as_uint(x0) | ((uint64_t)__float_as_uint(x1) << 32);
-        };
+        const float e = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mt);
+        lt = __builtin_fmaf(e, lw[w], lt);
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
-            __hip_atomic_store(so + (2 * d) * kWave + lane, pack(o[d][0], o[d][1]),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(so + (2 * d + 1) * kWave + lane, pack(o[d][2], o[d][3]),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const f32x4 x = sO[w][d][lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ot[d][i] = __builtin_fmaf(e, x[i], ot[d][i]);
         }
-        __hip_atomic_store(so + DecodeSlot<D>::O * kWave + lane, pack(m, l), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the slot before the count
-        uint32_t ticket = 0;
-        if (lane == 0)
-            ticket = __hip_atomic_fetch_add(a.counters + item, 1u, __ATOMIC_ACQ_REL,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-        ticket = __shfl(ticket, 0);
-        if (ticket != (uint32_t)(parts - 1)) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other parts' slots
-        if (lane == 0)
-            __hip_atomic_store(a.counters + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        auto get = [](const uint64_t *q) {
-            return __hip_atomic_load(const_cast<uint64_t *>(q), __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-        };
-        auto lo32 = [](uint64_t v) { return __uint_as_float((uint32_t)v); };
-        auto hi32 = [](uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); };
-        float mt = m;
-        for (int p = 0; p < parts; ++p)
-            if (p != self)
-                mt = fmaxf(mt, lo32(get(slots + (int64_t)p * DecodeSlot<D>::ELEMS +
-                                        DecodeSlot<D>::O * kWave + lane)));
-        float lt = 0.0f;
-        f32x4 tot[DB];
+    }
+    m = mt;
+    l = lt;
 #pragma unroll
-        for (int d = 0; d < DB; ++d) tot[d] = f32x4{};
-        for (int p = 0; p < parts; ++p) {
-            float mp, lp;
-            f32x4 op[DB];
-            if (p == self) {
-                mp = m;
-                lp = l;
+    for (int d = 0; d < DB; ++d) o[d] = ot[d];
+}
+
+// Balanced decode. The launch's work is the keys of all items (sequence, kv head)
+// cut into 64-key blocks; each item counts at least one block. With at most
+// kPlanItems items, every workgroup computes the prefix of the items' block counts
+// (from the context lengths, in LDS) and takes an equal run of blocks, whatever
+// the lengths; otherwise it takes an equal run of whole items. Within a run, each
+// item's part is one segment: the 4 waves take its blocks in turn (wave w: blocks
+// w, w + 4, ...), keep a flash-decoding running state and merge in LDS. An item
+// inside one workgroup's run is stored directly. An item spread over several
+// workgroups leaves one part per workgroup (the first or the last segment of a
+// run) in the workspace; the last part to arrive merges them all.
+template <int D, bool PAGED>
+__global__ __launch_bounds__(kDecodeWaves * 64, kWgPerCu) void decode_kernel(DecodeArgs a,
+                                                                             float *out) {
+    constexpr int DB = D / 16;   // 16-wide output blocks
+    __shared__ int32_t sOff[kPlanItems + 1];
+    __shared__ int32_t sWave[kDecodeWaves];
+    __shared__ f32x4 sO[kDecodeWaves][DB][kWave];
+    __shared__ float2 sML[kDecodeWaves * kWave];
+    __shared__ uint32_t sLast;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const int g = blockIdx.x;
+    const int64_t G = a.wgs;
+
+    if (a.flat) plan_blocks(a, sOff, sWave);
+    // Values read from LDS arrive in vector registers; every one of them is uniform
+    // over the workgroup, and moving them to scalar registers keeps the loop control
+    // and the addresses scalar.
+    const int64_t T = a.flat ? __builtin_amdgcn_readfirstlane(sOff[a.items]) : a.items;
+    auto unit_of = [&](int item) -> int64_t {
+        return a.flat ? __builtin_amdgcn_readfirstlane(sOff[item]) : item;
+    };
+    const int64_t u0 = wg_start(g, T, G), u1 = wg_start(g + 1, T, G);
+    if (u0 >= u1) return;  // no units for this workgroup (uniform)
+    // First item of the run: the last item whose first unit is <= u0.
+    int item = (int)u0;
+    if (a.flat) {
+        int lo_i = 0, hi_i = a.items - 1;
+        while (lo_i < hi_i) {
+            const int mid = (lo_i + hi_i + 1) >> 1;
+            if (sOff[mid] <= u0) lo_i = mid; else hi_i = mid - 1;
+        }
+        item = __builtin_amdgcn_readfirstlane(lo_i);
+    }
+
+    for (;;) {
+        const int64_t p_begin = unit_of(item), p_end = unit_of(item + 1);
+        ItemKeys ik = item_keys(a, item);
+        // The item is the workgroup's: its length moves to a scalar register.
+        ik.len = __builtin_amdgcn_readfirstlane(ik.len);
+        ik.lo = __builtin_amdgcn_readfirstlane(ik.lo);
+        ik.first_block = __builtin_amdgcn_readfirstlane(ik.first_block);
+        ik.blocks = __builtin_amdgcn_readfirstlane(ik.blocks);
+        const int b = item / a.kv_heads, kvh = item % a.kv_heads;
+        // This segment's blocks of the item (local numbering).
+        const int s_blk = a.flat ? (int)(max(u0, p_begin) - p_begin) : 0;
+        const int e_blk = a.flat ? (int)(min(u1, p_end) - p_begin) : ik.blocks;
+        if (ik.bad && s_blk == 0 && threadIdx.x == 0)
+            flag_status(a.status, REEF_STATUS_BIT_BAD_LENGTH);
+
+        const int head = kvh * a.group + col;   // this lane's query head (live if col < group)
+        const bool head_ok = col < a.group;
+        const int k_begin = (ik.first_block + s_blk + wave) * kBlockKeys;
+        const int k_end = min(ik.len, (ik.first_block + e_blk) * kBlockKeys);
+        const int n_pages = (ik.len + kPage - 1) / kPage;
+        i32x4 qop[D / 64];
+        const float c = load_query<D>(a, b, head, head_ok, grp, qop);
+        DecodeRun<D> st;
+        reset_run<D>(st);
+        bool bad_page = false;
+        run_keys<D, PAGED>(a, b, kvh, ik.lo, k_begin, k_end, kDecodeWaves * kBlockKeys, n_pages,
+                           qop, c, lane, st, bad_page);
+        if (bad_page) flag_status(a.status, REEF_STATUS_BIT_BAD_PAGE);
+        // Row sums: this lane holds head col's partial over its 16 keys per block.
+        float l = st.l_run;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        float m = st.m_run;
+        f32x4 o[DB];
 #pragma unroll
-                for (int d = 0; d < DB; ++d) op[d] = o[d];
+        for (int d = 0; d < DB; ++d) o[d] = st.acc[d] * st.s_run;
+        merge_waves<D>(m, l, o, sO, sML, wave, lane);
+
+        // Workgroups holding a part of this item: the non-empty ones in gf .. gl.
+        // With T >= G every workgroup owns at least one unit; with fewer units than
+        // workgroups each non-empty one owns exactly one.
+        const int gf = a.flat ? wg_of(p_begin, T, G) : g;
+        const int gl = a.flat ? wg_of(p_end - 1, T, G) : g;
+        const int parts = T >= G ? gl - gf + 1 : (int)(p_end - p_begin);
+        if (wave == 0) {
+            if (parts == 1) {
+                // A sequence with no keys (a bad length) ends with l = 0 and stores zeros.
+                if (head_ok) {
+                    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+                    float *orow = out + ((int64_t)b * a.q_heads + head) * D;
+#pragma unroll
+                    for (int d = 0; d < DB; ++d)
+                        *reinterpret_cast<f32x4 *>(orow + 16 * d + 4 * grp) = o[d] * inv;
+                }
             } else {
-                const uint64_t *sl = slots + (int64_t)p * DecodeSlot<D>::ELEMS;
-                const uint64_t ml = get(sl + DecodeSlot<D>::O * kWave + lane);
-                mp = lo32(ml);
-                lp = hi32(ml);
+                // Part slot: 0 for the first segment of this run, 1 for the last. The
+                // slots are written with agent-scope atomic stores (coherent at the
+                // device level, beneath the per-XCD L2s), which have completed
+                // (vmcnt 0) before the item's counter counts this part in; the part
+                // that counts last reads the slots with agent-scope atomic loads
+                // issued after its count returned. Every access to the shared data is
+                // device-coherent, so no L2 write-back or invalidate is needed.
+                const int slot = p_begin <= u0 ? 0 : 1;
+                uint64_t *so = reinterpret_cast<uint64_t *>(a.slots) +
+                               ((int64_t)g * 2 + slot) * DecodeSlot<D>::ELEMS;
+                auto pack = [](float x0, float x1) {
+                    return (uint64_t)__float_as_uint(x0) | ((uint64_t)__float_as_uint(x1) << 32);
+                };
+                if (head_ok) {
 #pragma unroll
-                for (int d = 0; d < DB; ++d) {
-                    const uint64_t v0 = get(sl + (2 * d) * kWave + lane);
-                    const uint64_t v1 = get(sl + (2 * d + 1) * kWave + lane);
-                    op[d] = f32x4{lo32(v0), hi32(v0), lo32(v1), hi32(v1)};
+                    for (int d = 0; d < DB; ++d) {
+                        __hip_atomic_store(so + (2 * d) * kWave + lane, pack(o[d][0], o[d][1]),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(so + (2 * d + 1) * kWave + lane, pack(o[d][2], o[d][3]),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    __hip_atomic_store(so + DecodeSlot<D>::O * kWave + lane, pack(m, l),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_s_waitcnt(0);  // vmcnt 0: every slot store has completed
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                uint32_t ticket = 0;
+                if (lane == 0)
+                    ticket = __hip_atomic_fetch_add(a.counters + item, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+                ticket = __shfl(ticket, 0);
+                if (lane == 0) sLast = ticket == (uint32_t)(parts - 1) ? 1u : 0u;
+            }
+        }
+        __syncthreads();  // frees sO / sML, publishes sLast
+        if (parts > 1 && __builtin_amdgcn_readfirstlane(sLast)) {
+            // Every wave merges the parts gf + wave, gf + wave + 4, ... in order, then
+            // the waves merge in LDS: the same result whichever part arrived last.
+            const int64_t first_start = wg_start(gf, T, G);
+            float mp_run = -INFINITY, lp_run = 0.0f;
+            f32x4 op_run[DB];
+#pragma unroll
+            for (int d = 0; d < DB; ++d) op_run[d] = f32x4{};
+            auto get = [](const uint64_t *q) {
+                return __hip_atomic_load(const_cast<uint64_t *>(q), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            };
+            auto lo32 = [](uint64_t v) { return __uint_as_float((uint32_t)v); };
+            auto hi32 = [](uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); };
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (head_ok) {
+                for (int gg = gf + wave; gg <= gl; gg += kDecodeWaves) {
+                    if (wg_start(gg, T, G) == wg_start(gg + 1, T, G)) continue;  // empty
+                    const int slot = gg == gf && first_start < p_begin ? 1 : 0;
+                    const uint64_t *sl = reinterpret_cast<const uint64_t *>(a.slots) +
+                                         ((int64_t)gg * 2 + slot) * DecodeSlot<D>::ELEMS;
+                    const uint64_t ml = get(sl + DecodeSlot<D>::O * kWave + lane);
+                    f32x4 op[DB];
+#pragma unroll
+                    for (int d = 0; d < DB; ++d) {
+                        const uint64_t v0 = get(sl + (2 * d) * kWave + lane);
+                        const uint64_t v1 = get(sl + (2 * d + 1) * kWave + lane);
+                        op[d] = f32x4{lo32(v0), hi32(v0), lo32(v1), hi32(v1)};
+                    }
+                    const float mp = lo32(ml), lp = hi32(ml);
+                    const float mn = fmaxf(mp_run, mp);
+                    const float er = mp_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp_run - mn);
+                    const float ep = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - mn);
+                    lp_run = __builtin_fmaf(ep, lp, lp_run * er);
+#pragma unroll
+                    for (int d = 0; d < DB; ++d)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            op_run[d][i] = __builtin_fmaf(ep, op[d][i], op_run[d][i] * er);
+                    mp_run = mn;
                 }
             }
-            const float wp = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - mt);
-            lt = __builtin_fmaf(wp, lp, lt);
+            merge_waves<D>(mp_run, lp_run, op_run, sO, sML, wave, lane);
+            if (wave == 0) {
+                if (lane == 0)
+                    __hip_atomic_store(a.counters + item, 0u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                if (head_ok) {
+                    const float inv = lp_run > 0.0f ? 1.0f / lp_run : 0.0f;
+                    float *orow = out + ((int64_t)b * a.q_heads + head) * D;
 #pragma unroll
-            for (int d = 0; d < DB; ++d)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) tot[d][i] = __builtin_fmaf(wp, op[d][i], tot[d][i]);
+                    for (int d = 0; d < DB; ++d)
+                        *reinterpret_cast<f32x4 *>(orow + 16 * d + 4 * grp) = op_run[d] * inv;
+                }
+            }
+            __syncthreads();  // frees sO / sML
         }
-#pragma unroll
-        for (int d = 0; d < DB; ++d) o[d] = tot[d];
-        l = lt;
-        store = true;
-    }
-    // A sequence with no keys (a bad length) ends with l = 0 and stores zeros.
-    if (store && head_ok) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float *orow = out + ((int64_t)b * a.q_heads + head) * D;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) *reinterpret_cast<f32x4 *>(orow + 16 * d + 4 * grp) = o[d] * inv;
+        if (p_end >= u1) break;
+        ++item;
     }
 }
 
@@ -534,18 +664,25 @@ __global__ void pack_v_pages(const int8_t *__restrict__ v_tokens, int64_t pages,
         *reinterpret_cast<const i32x4 *>(buf);
 }
 
-int default_splits(const reef_decode_params *p) {
-    if (p->num_splits > 0) return p->num_splits;
-    const int64_t blocks = ceil_div(p->max_context, kBlockKeys);
-    const int64_t pairs = p->batch * p->kv_heads;
-    // About 1024 waves (4 per compute unit) with 16 KB of cache in flight each
-    // keep HBM busy; more add per-split start-up and merge work. At least one
-    // full workgroup (4 splits) per sequence, at least 4 blocks (256 keys) per
-    // split. Measured on MI355X, 128 x 8q/1kv ragged paged: 43 us at 8 splits,
-    // 45 us at 16; 4 x 8kv x 32768: 53 us at 32, 61 us at 64.
-    int64_t s = std::max<int64_t>(kDecodeWaves, ceil_div(1024, pairs));
-    s = std::min<int64_t>(s, ceil_div(blocks, 4));
-    return (int)std::max<int64_t>(1, s);
+// Whether the launch deals out 64-key blocks (the items' prefix fits the LDS plan
+// and the block count of the largest possible launch fits 31 bits).
+bool flat_plan(const reef_decode_params *p) {
+    const int64_t items = p->batch * p->kv_heads;
+    return items <= kPlanItems && items * ceil_div(p->max_context, kBlockKeys) < (int64_t(1) << 31);
+}
+
+// Workgroups of the launch: two per compute unit (8 waves, each with 16 KB of
+// cache in flight, keep HBM busy), or one per unit of work when there are fewer
+// (a workgroup that takes several items in turn pays each item's start-up and
+// merge latency once more: 128 one-block items took 66 us on 8 workgroups, 8 us
+// on 128). num_splits > 0 asks for that many waves per item on average instead.
+// Measured on MI355X at 128 x 8q/1kv ragged paged and 64 x 8kv x 4096 contiguous.
+int64_t decode_wgs(const reef_decode_params *p) {
+    const int64_t items = p->batch * p->kv_heads;
+    const int64_t units = flat_plan(p) ? items * ceil_div(p->max_context, kBlockKeys) : items;
+    const int64_t g = p->num_splits > 0 ? ceil_div(items * p->num_splits, kDecodeWaves)
+                                        : kWgPerCu * compute_units();
+    return std::max<int64_t>(1, std::min<int64_t>(std::min(g, units), 1 << 20));
 }
 
 reef_status validate_params(const reef_decode_params *p, const int8_t *q, const float *q_scales,
@@ -559,6 +696,7 @@ reef_status validate_params(const reef_decode_params *p, const int8_t *q, const 
         return REEF_INVALID_ARGUMENT;
     if (p->head_dim != 64 && p->head_dim != 128) return REEF_UNSUPPORTED;
     if (p->q_heads / p->kv_heads > 16 || p->kv_heads > 65535 || p->batch > 65535 ||
+        p->batch * p->kv_heads > INT32_MAX ||
         p->max_context >= (int64_t(1) << 30))
         return REEF_UNSUPPORTED;
     if (!aligned(q, 16) || !aligned(out, 4)) return REEF_INVALID_ARGUMENT;
@@ -575,16 +713,15 @@ reef_status validate(const reef_decode_params *p, const int8_t *q, const float *
     return REEF_OK;
 }
 
-// Workspace: one counter per (sequence, kv head), then, with more than one
-// workgroup (4 splits) per sequence, one part slot per workgroup.
+// Workspace: one counter per (sequence, kv head), then, when blocks are dealt
+// out, two part slots per workgroup (the first and the last segment of its run).
 int64_t counter_bytes(const reef_decode_params *p) {
     return ceil_div(p->batch * p->kv_heads * 4, 256) * 256;
 }
 
 int64_t workspace_bytes(const reef_decode_params *p) {
-    const int64_t groups = ceil_div(default_splits(p), kDecodeWaves);
     const int64_t slot = (p->head_dim == 128 ? DecodeSlot<128>::ELEMS : DecodeSlot<64>::ELEMS) * 8;
-    return counter_bytes(p) + (groups > 1 ? p->batch * p->kv_heads * groups * slot : 0);
+    return counter_bytes(p) + (flat_plan(p) ? decode_wgs(p) * 2 * slot : 0);
 }
 
 template <bool PAGED>
@@ -598,12 +735,12 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
     a.window = (int32_t)std::min<int64_t>(p->window, INT32_MAX);
     a.q_gran = p->q_granularity;
     a.score_scale = p->softmax_scale * kLog2e;
-    const int splits = default_splits(p);
-    a.splits = splits;
-    a.groups = (int32_t)ceil_div(splits, kDecodeWaves);
+    a.items = (int32_t)(p->batch * p->kv_heads);
+    a.flat = flat_plan(p) ? 1 : 0;
+    a.wgs = (int32_t)decode_wgs(p);
     a.counters = static_cast<uint32_t *>(workspace);
     a.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + counter_bytes(p));
-    const dim3 grid((unsigned)a.groups, (unsigned)p->kv_heads, (unsigned)p->batch);
+    const dim3 grid((unsigned)a.wgs);
     if (p->head_dim == 128)
         hipLaunchKernelGGL((decode_kernel<128, PAGED>), grid, dim3(64 * kDecodeWaves), 0, stream, a,
                            out);
@@ -657,7 +794,7 @@ namespace {
 // by every call on that GPU. In host code `scratch` is a stand-in symbol, not a
 // device address: scratch_address() resolves the device address once per device
 // (with that device current) and every use goes through it.
-constexpr int64_t kScratchBytes = int64_t(8) << 20;
+constexpr int64_t kScratchBytes = int64_t(16) << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;

@@ -98,12 +98,18 @@ def test_decode_host_validation_and_workspace():
     p = DecodeParams(batch=64, q_heads=32, kv_heads=8, head_dim=128, max_context=4096,
                      window=0, softmax_scale=0.1, q_granularity=2, num_splits=0, flags=0)
     ws = lib.reef_attention_decode_workspace_bytes(C.byref(p))
-    # one counter per (sequence, kv head); 4 splits per sequence are one workgroup,
-    # so no part slots
-    assert ws == 2048
+    # one counter per (sequence, kv head), then two part slots (64 lanes x 17
+    # eight-byte words) per workgroup: 2 workgroups per compute unit (256 without a
+    # GPU), the 512 items' 64-key blocks dealt out among them
+    slot = 17 * 64 * 8
+    assert ws == 2048 + 512 * 2 * slot
     many = DecodeParams(64, 32, 8, 128, 4096, 0, 0.1, 2, 9, 0)
-    # 9 splits: 3 workgroups per sequence, each with a slot of 64 lanes x 17 eight-byte words
-    assert lib.reef_attention_decode_workspace_bytes(C.byref(many)) == 2048 + 64 * 8 * 3 * 17 * 64 * 8
+    # num_splits 9: 512 items x 9 / 4 waves = 1152 workgroups
+    assert lib.reef_attention_decode_workspace_bytes(C.byref(many)) == 2048 + 1152 * 2 * slot
+    # more items than the in-workgroup plan holds (2048): whole items per workgroup,
+    # no part slots
+    big = DecodeParams(4096, 8, 1, 128, 4096, 0, 0.1, 2, 0, 0)
+    assert lib.reef_attention_decode_workspace_bytes(C.byref(big)) == 4096 * 4
     f = [_fake(i) for i in range(1, 12)]
     args = lambda pp, w: (C.byref(pp), f[0], f[1], f[2], f[3], f[4], f[5], None, f[6], f[7],  # noqa: E731
                           w, None, None)

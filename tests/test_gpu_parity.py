@@ -538,20 +538,23 @@ def test_decode_paged_matches_oracle(reef, B, Hq, Hkv, D, lens, window):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("paged,B,Hq,Hkv,D,window", [
-    (False, 300, 4, 2, 128, 0),   # 300 sequences x 2 kv heads
-    (True, 130, 8, 1, 128, 0),    # ragged pool, 8:1 grouping
-    (True, 40, 16, 2, 64, 300),   # window
+@pytest.mark.parametrize("paged,B,Hq,Hkv,D,window,max_len", [
+    (False, 300, 4, 2, 128, 0, 1500),   # 300 sequences x 2 kv heads
+    (True, 130, 8, 1, 128, 0, 1500),    # ragged pool, 8:1 grouping
+    (True, 40, 16, 2, 64, 300, 1500),   # window
+    (True, 24, 8, 1, 128, 0, 8192),     # lengths up to 8192: items over many workgroups
+    (False, 2100, 2, 1, 64, 0, 64),     # more items than the block plan holds: whole items
 ])
-def test_decode_ragged_merge_in_launch(reef, paged, B, Hq, Hkv, D, window):
-    """Sequences split over several workgroups are merged by the last of them in the
-    same launch: oracle tolerance, bit-identical on a second call (fixed merge
-    order), item counters back at zero, and another split count agrees."""
+def test_decode_ragged_merge_in_launch(reef, paged, B, Hq, Hkv, D, window, max_len):
+    """Sequences whose keys are dealt out over several workgroups are merged by the
+    last of them in the same launch: oracle tolerance, bit-identical on a second
+    call (fixed merge order), item counters back at zero, and another split count
+    agrees."""
     rng = np.random.default_rng(B + D)
-    lens = [int(x) for x in rng.integers(1, 1500, B)]
-    lens[0], lens[-1] = 1, 1500
+    lens = [int(x) for x in rng.integers(1, max_len, B)]
+    lens[0], lens[-1] = 1, max_len
     max_ctx = ((max(lens) + 63) // 64) * 64
-    case(f"decode ragged paged={paged} B{B} Hq{Hq} Hkv{Hkv} D{D} win{window}")
+    case(f"decode ragged paged={paged} B{B} Hq{Hq} Hkv{Hkv} D{D} win{window} max_len{max_len}")
     qq, qs, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 61 + B, max_ctx)
     scale = 1 / math.sqrt(D)
     glens = gpu(np.array(lens, np.int32))

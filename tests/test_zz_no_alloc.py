@@ -1,8 +1,9 @@
 """The allocation-free paged decode (reef_attention_decode_int8_paged_noalloc)
 against the paged decode with a caller workspace: bit-identical outputs on two
 calls in a row (the second smaller, so the scratch array holds the first call's
-counters and slots when it starts), both with sequences split over several
-workgroups so that the part slots and counters in the scratch array are used."""
+counters and slots when it starts), both with sequences whose keys are dealt out
+over several workgroups so that the part slots and counters in the scratch array
+are used."""
 import ctypes as C
 import math
 
@@ -78,8 +79,8 @@ def _run(reef, x, B, Hq, Hkv, D, noalloc, num_splits=0):
 
 def test_noalloc_matches_workspace_entry_point_on_two_calls(reef):
     D = 128
-    # first call: 40 sequences x 2 kv heads, lengths up to 1500 (two workgroups per
-    # sequence merge through the scratch slots)
+    # first call: 40 sequences x 2 kv heads, lengths up to 1500 (their 64-key blocks
+    # dealt out over 120 workgroups: the long sequences merge through the scratch slots)
     lens1 = [int(x) for x in np.random.default_rng(1).integers(1, 1500, 40)]
     lens1[0], lens1[-1] = 1500, 1
     x1 = _problem(11, 40, 8, 2, D, lens1)
@@ -90,7 +91,7 @@ def test_noalloc_matches_workspace_entry_point_on_two_calls(reef):
     assert reef.lib().reef_attention_decode_workspace_bytes(C.byref(p1)) > 80 * 2 * 17 * 64 * 8
     assert np.isfinite(a1).all()
     assert np.array_equal(a1.view(np.uint32), r1.view(np.uint32))
-    # second call, smaller: 7 sequences, 1 kv head, 3 workgroups per sequence
+    # second call, smaller: 7 sequences, 1 kv head, num_splits 9 (16 workgroups)
     lens2 = [900, 17, 1024, 3, 640, 511, 1000]
     x2 = _problem(12, 7, 8, 1, D, lens2)
     print("[case] noalloc decode call 2: B7 8q/1kv, 9 splits", flush=True)
@@ -104,11 +105,11 @@ def test_noalloc_matches_workspace_entry_point_on_two_calls(reef):
 
 
 def test_noalloc_rejects_workspace_beyond_scratch(reef):
-    """A shape whose split-merge workspace exceeds the 8 MiB scratch array is
+    """A shape whose split-merge workspace exceeds the 16 MiB scratch array is
     refused before any launch."""
     lib = reef.lib()
-    p = reef.DecodeParams(4096, 8, 8, 128, 8192, 0, 0.1, reef.PER_HEAD, 64, 0)
-    assert lib.reef_attention_decode_workspace_bytes(C.byref(p)) > 8 << 20
+    p = reef.DecodeParams(2048, 8, 1, 128, 8192, 0, 0.1, reef.PER_HEAD, 64, 0)
+    assert lib.reef_attention_decode_workspace_bytes(C.byref(p)) > 16 << 20
     f = lambda n: C.c_void_p(0x10000 * n)  # noqa: E731
     rc = lib.reef_attention_decode_int8_paged_noalloc(C.byref(p), f(1), f(2), f(3), f(4), f(5), f(6),
                                                       f(7), 512, 100, f(8), f(9), None, None)
