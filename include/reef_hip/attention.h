@@ -210,7 +210,9 @@ reef_status reef_qk_scores_i32(const int8_t *q, const int8_t *k, int64_t batch, 
  * table: 256 uint16 on the device (exp_table(), :156-164). q, k, v int8
  * [B, H, S, D] with strides as for the prefill; out int8 [B, Hq, q_len, D].
  * p->softmax_scale, q_granularity, kv_granularity and flags are not used;
- * head_dim 32, 64 or 128; score_shift and out_shift at most 31. */
+ * head_dim 32, 64 or 128; score_shift and out_shift at most 31. A row may see at
+ * most 65536 keys (kv_len, or the window when shorter): beyond that the engine's
+ * uint32 weight sum could wrap, and the call returns REEF_UNSUPPORTED. */
 reef_status reef_attention_int8_integer(const reef_attention_params *p, const int8_t *q,
                                         const reef_strides *q_strides, const int8_t *k,
                                         const reef_strides *k_strides, const int8_t *v,

@@ -29,6 +29,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kIntThreads = 256;  // 4 waves x 32 query rows
 constexpr int kIntRows = 128;
 constexpr int kIntKeys = 64;  // keys per tile
+// Most keys a row may see: 65536 x 65535 (the largest table weight) < 2^32, so
+// no row's weight sum wraps.
+constexpr int64_t kMaxIntKeys = 65536;
 
 struct IntHeadArgs {
     const int8_t *q, *k, *v;
@@ -370,6 +373,11 @@ extern "C" reef_status reef_attention_int8_integer(
         return REEF_INVALID_ARGUMENT;
     if (D != 32 && D != 64 && D != 128) return REEF_UNSUPPORTED;
     if (p->kv_len >= (int64_t(1) << 30) || p->window >= (int64_t(1) << 30)) return REEF_UNSUPPORTED;
+    // A row's weight sum is a uint32 of at most (visible keys) x 65535. Beyond 65536
+    // visible keys the engine's sum could wrap, and the kernel's shortcuts (24-bit
+    // multiply-adds, one rounding step, no clamp) hold only while it does not.
+    const int64_t visible = p->window > 0 ? std::min<int64_t>(p->window, p->kv_len) : p->kv_len;
+    if (visible > kMaxIntKeys) return REEF_UNSUPPORTED;
     if (!int8_strides_ok(q_strides, q) || !int8_strides_ok(k_strides, k) ||
         !int8_strides_ok(v_strides, v) || !aligned(out, 4))
         return REEF_INVALID_ARGUMENT;

@@ -131,3 +131,16 @@ def test_quantize_host_validation():
     assert lib.reef_quantize_int8_per_head(None, 1, 1, 1, 1, None, _fake(), _fake(), None,
                                            None) == 1
     assert lib.reef_read_status_word(None, 0, None) == 1
+
+
+def test_integer_head_refuses_rows_beyond_65536_keys():
+    """A row's uint32 weight sum (up to 65535 per key) cannot wrap within 65536
+    visible keys; longer rows (kv_len, or the window when it is shorter) are refused
+    before any launch."""
+    lib = reef_amd.lib()
+    f = [_fake(i) for i in range(1, 8)]
+    for kv_len, window in ((65537, 0), (70000, 65537)):
+        p = reef_amd.AttentionParams(1, 1, 1, 1, kv_len, 64, kv_len - 1, window, 1.0, 1, 1, 0)
+        rc = lib.reef_attention_int8_integer(C.byref(p), f[0], None, f[1], None, f[2], None, 10,
+                                             f[3], 8, f[4], None, None)
+        assert rc == reef_amd.UNSUPPORTED

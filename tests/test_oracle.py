@@ -441,3 +441,24 @@ def test_attention_int8_rejects_invalid_problems():
                               np.zeros((1, 2, 2, 8), np.int8), np.zeros((1, 2, 2, 8), np.int8),
                               np.ones(3, np.float32), np.ones(2, np.float32),
                               np.ones(2, np.float32))
+
+
+@pytest.mark.parametrize("n,want", [(65536, 0), (131073, 2)])
+def test_int8_softmax_weight_sum_wraps_like_the_engine(n, want):
+    """The engine sums a row's table weights in uint32 (int8.hpp:208-217). With the
+    engine's table (first entry 32768) and n equal keys the sum is n * 32768: exact
+    at 65536 keys (2^31: the reciprocal (255 << 16) / sum is 0, every probability 0),
+    wrapped to 32768 at 131073 (reciprocal 510, every probability clamped to 255, so
+    255 * 131073 shifted right by 24 rounds to 2). The oracle keeps the wrap, checked
+    against the engine's own code where it is built. The device path refuses rows
+    with more than 65536 visible keys, so past that boundary only the oracle runs."""
+    d = 32
+    q = np.zeros((1, d), np.int8)
+    k = np.zeros((n, d), np.int8)
+    v = np.ones((n, d), np.int8)
+    out = oracle.attend_head_int8(q, k, v, n - 1, 0, 0, 24)
+    assert (out == want).all()
+    if oracle.ref_available():
+        ref = np.empty((1, d), np.int8)
+        assert oracle.ref().ref_attend_head_int8(q, k, v, 1, n, d, n - 1, 0, 0, 24, ref) == 0
+        assert np.array_equal(out, ref)
