@@ -49,7 +49,7 @@ def build() -> None:
     if os.path.isdir(os.environ.get("REEF_REFERENCE", "/root/reference/inference-engine")):
         subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
         if os.path.exists(os.path.join(HERE, "..", "reef_amd", "libreef_hip.so")):
-            subprocess.run(["make", "-s", "-C", HERE, "dropin"], check=True)
+            subprocess.run(["make", "-s", "-C", HERE, "dropin", "gpt_neo"], check=True)
 
 
 def _load() -> C.CDLL:

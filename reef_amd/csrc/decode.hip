@@ -281,14 +281,21 @@ __device__ __forceinline__ void block_math(const DecodeBlock<D> &cur, int kb, in
     }
     const float m_use = st.m_run == -INFINITY ? 0.0f : st.m_run;
 
-    // P operand: lane group g's keys 16g + 8h + e for the two halves h.
-    f16x8 pop[2];
+    // P operand: lane group g's keys 16g + 8h + e for the two halves h, each weight
+    // p * v_scale / s_run split into an fp16 part and the fp16 of its remainder
+    // (22 significant bits together: one fp16 alone moves an output by up to
+    // 2^-12 of the values' magnitude, about 1e-3 for |v| ~ 4). The products run
+    // on both; the row sum stays the fp32 sum of p.
+    f16x8 pop[2], plo[2];
     float lp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const float p = __builtin_amdgcn_exp2f(x[r] - m_use);
         lp[r & 3] += p;
-        pop[r >> 3][r & 7] = (_Float16)(p * (vv[r] * st.inv_s));
+        const float w = p * (vv[r] * st.inv_s);
+        const _Float16 hi = (_Float16)w;
+        pop[r >> 3][r & 7] = hi;
+        plo[r >> 3][r & 7] = (_Float16)(w - (float)hi);
     }
     st.l_run += (lp[0] + lp[1]) + (lp[2] + lp[3]);
     // out^T = V^T . P^T: the output column is the head (lane % 16), the lane
@@ -298,7 +305,9 @@ __device__ __forceinline__ void block_math(const DecodeBlock<D> &cur, int kb, in
         f16x8 v0, v1;
         int8x16_to_f16(vop[d], v0, v1);
         st.acc[d] = mfma_16x16x32_f16(v0, pop[0], st.acc[d]);
+        st.acc[d] = mfma_16x16x32_f16(v0, plo[0], st.acc[d]);
         st.acc[d] = mfma_16x16x32_f16(v1, pop[1], st.acc[d]);
+        st.acc[d] = mfma_16x16x32_f16(v1, plo[1], st.acc[d]);
     }
 }
 

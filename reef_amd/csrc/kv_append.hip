@@ -18,7 +18,6 @@ namespace {
 
 constexpr int kPage = 16;
 constexpr int kAppendThreads = 256;  // 4 waves per (batch, kv head, cache page)
-constexpr int kAppendWaves = kAppendThreads / kWave;
 
 struct AppendArgs {
     const float *k, *v;

@@ -94,10 +94,7 @@ struct StreamSlot {  // floats of one partial result: output in lane order, then
 
 // Row m of a 32-row score block holds key sigma(m) = 16 ((m >> 2) & 1) +
 // 4 (m >> 3) + (m & 3), so that output register r = 4j + i of lane group g is
-// key 16g + r. Inverse: key kk -> row.
-__device__ __forceinline__ int score_row_of_key(int kk) {
-    return ((kk >> 2) & 3) * 8 + (kk >> 4) * 4 + (kk & 3);
-}
+// key 16g + r.
 __device__ __forceinline__ int key_of_score_row(int m) {
     return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
 }
@@ -451,7 +448,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             mt = xor32_max(mt);
             float svt = 0.0f;
             bool grow = mt > m_run + kLazy;
-            if (KV_TOKEN) {
+            if constexpr (KV_TOKEN) {
                 svt = sScale[buf][2 * kBN];
                 grow = grow || svt > s_run * 16.0f;
             }

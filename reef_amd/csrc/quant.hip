@@ -484,12 +484,6 @@ __global__ __launch_bounds__(kQuantThreads) void dequantize(const int8_t *__rest
     }
 }
 
-int grid_for(int64_t work_items, int64_t cap = 4096) {
-    int64_t g = ceil_div(work_items, kQuantThreads);
-    if (g < 1) g = 1;
-    return (int)(g < cap ? g : cap);
-}
-
 // The flat kernels over f (q 4-byte aligned, at least 4 * batch * heads * blocks
 // bytes): two launches when the shortest chunk of q holds a head's batch * blocks
 // partial words, three otherwise.
