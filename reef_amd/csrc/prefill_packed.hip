@@ -378,7 +378,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         return out;
     };
     // Tile j: masks, the lazy rescale, the probabilities and their row sums, P.V.
-    auto tile_math = [&](const int j, auto masked_tag, Scores sc) {
+    auto tile_math = [&](const int j, auto masked_tag, Scores sc, auto &&after_rescale) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int kt = kt0 + kPK * j;
         bool need = false;
@@ -411,6 +411,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
 #pragma unroll
             for (int d = 0; d < DB; ++d) acc[d] *= alpha;
         }
+        after_rescale();
         // Per chunk of 16 keys: the probabilities, their fp16 row sums, then the
         // products (the residual products of the value blocks that need them right
         // after, so that a chunk's residuals die with it).
@@ -487,15 +488,17 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     const int it_a = max(0, wg_full_lo - kt0 + kPK - 1) / kPK;
     const int span = wg_full_hi + 1 - kt0;
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kPK : 0));
-    // Tile j's softmax and products with the scores of tile j + 1 issued first; returns
-    // those scores.
+    // Tile j's softmax and products, with the scores of tile j + 1 issued between the
+    // rescale and the probabilities, in the same straight-line code as tile j's
+    // products, so that the matrix and vector instructions interleave; returns those
+    // scores. Past the last tile they are computed from a stale K slot (no slot is
+    // being written at that point) and discarded.
     auto step = [&](const int j, auto masked_tag, const Scores &cur) {
         wait_loads(group_loads(j + 1));
         __builtin_amdgcn_s_barrier();
         issue_group(j + 2);
-        Scores next{};
-        if (j + 1 < n_tiles) next = scores(j + 1);  // on the matrix cores beside the softmax
-        tile_math(j, masked_tag, cur);
+        Scores next;
+        tile_math(j, masked_tag, cur, [&] { next = scores(j + 1); });
         return next;
     };
     // Two tiles per iteration: the loop-carried scores come back in the registers
