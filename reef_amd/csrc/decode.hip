@@ -484,19 +484,25 @@ __global__ __launch_bounds__(kDecodeWaves * 64, kWgPerCu) void decode_kernel(Dec
     const int g = blockIdx.x;
     const int64_t G = a.wgs;
 
-    if (a.flat) plan_blocks(a, sOff, sWave);
+    // Without context lengths every item holds max_context keys: the same block
+    // count, so the prefix is i * nb and no plan is needed.
+    const bool same = a.context_lens == nullptr;
+    const int64_t nb = same ? item_keys(a, 0).blocks : 0;
+    if (a.flat && !same) plan_blocks(a, sOff, sWave);
     // Values read from LDS arrive in vector registers; every one of them is uniform
     // over the workgroup, and moving them to scalar registers keeps the loop control
     // and the addresses scalar.
-    const int64_t T = a.flat ? __builtin_amdgcn_readfirstlane(sOff[a.items]) : a.items;
+    const int64_t T = !a.flat ? a.items
+                      : same  ? a.items * nb
+                              : __builtin_amdgcn_readfirstlane(sOff[a.items]);
     auto unit_of = [&](int item) -> int64_t {
-        return a.flat ? __builtin_amdgcn_readfirstlane(sOff[item]) : item;
+        return !a.flat ? item : same ? item * nb : __builtin_amdgcn_readfirstlane(sOff[item]);
     };
     const int64_t u0 = wg_start(g, T, G), u1 = wg_start(g + 1, T, G);
     if (u0 >= u1) return;  // no units for this workgroup (uniform)
     // First item of the run: the last item whose first unit is <= u0.
-    int item = (int)u0;
-    if (a.flat) {
+    int item = (int)(a.flat && same ? u0 / nb : u0);
+    if (a.flat && !same) {
         int lo_i = 0, hi_i = a.items - 1;
         while (lo_i < hi_i) {
             const int mid = (lo_i + hi_i + 1) >> 1;
