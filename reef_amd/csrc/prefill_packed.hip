@@ -369,12 +369,19 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     auto scores = [&](int j) {  // scores of tile j, keys 32u .. 32u + 31 in u[u]
         const int8_t *sK = kring + (j % kSlots) * kKTile;
         Scores out;
+        i32x4 kop[2][kPD / 32];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int t = 0; t < kPD / 32; ++t)
-                out.u[u] = mfma_32x32x32_i8(*reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]),
-                                            qop[t], t == 0 ? (BIAS ? bias : i32x16{}) : out.u[u]);
+                kop[u][t] = *reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]);
+        
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int t = 0; t < kPD / 32; ++t)
+                out.u[u] = mfma_32x32x32_i8(kop[u][t], qop[t],
+                                            t == 0 ? (BIAS ? bias : i32x16{}) : out.u[u]);
         return out;
     };
     // Tile j: masks, the lazy rescale, the probabilities and their row sums, P.V.
@@ -421,6 +428,10 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 uint32_t phi[4], plo[4];
+                f16x8 vop[DB];
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                    vop[d] = *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[u][s]);
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) {
                     float p[2];
@@ -439,17 +450,12 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
                 rs_hi = mfma_16x16x32_f16(ones, operand(phi), rs_hi);
                 if (LO) rs_lo = mfma_16x16x32_f16(ones, operand(plo), rs_lo);
 #pragma unroll
-                for (int d = 0; d < DB; ++d)
-                    acc[d] = mfma_32x32x16_f16(
-                        *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[u][s]),
-                        operand(phi), acc[d]);
+                for (int d = 0; d < DB; ++d) acc[d] = mfma_32x32x16_f16(vop[d], operand(phi), acc[d]);
                 if (LO) {
 #pragma unroll
                     for (int d = 0; d < DB; ++d)
                         if ((pmask >> d) & 1)  // uniform
-                            acc[d] = mfma_32x32x16_f16(
-                                *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[u][s]),
-                                operand(plo), acc[d]);
+                            acc[d] = mfma_32x32x16_f16(vop[d], operand(plo), acc[d]);
                 }
             }
     };
