@@ -34,7 +34,7 @@ constexpr int kDecodeWaves = 4;          // waves per workgroup
 constexpr int kBlockKeys = 64;           // keys per inner step (4 pages)
 constexpr int kPage = 16;                // tokens per page
 constexpr int kPlanItems = 2048;         // items whose block offsets a workgroup plans in LDS
-constexpr int kWgPerCu = 2;              // resident workgroups per compute unit
+constexpr int kWgPerCu = 2;              // resident workgroups per compute unit (at most)
 
 struct DecodeArgs {
     const int8_t *q;
@@ -468,10 +468,11 @@ __device__ __forceinline__ void merge_waves(float &m, float &l, f32x4 (&o)[D / 1
 // w, w + 4, ...), keep a flash-decoding running state and merge in LDS. An item
 // inside one workgroup's run is stored directly. An item spread over several
 // workgroups leaves one part per workgroup (the first or the last segment of a
-// run) in the workspace; the last part to arrive merges them all.
+// run) in the workspace; the last part to arrive merges them all. A paged launch
+// places two workgroups on a compute unit, a contiguous one one (decode_wgs).
 template <int D, bool PAGED>
-__global__ __launch_bounds__(kDecodeWaves * 64, kWgPerCu) void decode_kernel(DecodeArgs a,
-                                                                             float *out) {
+__global__ __launch_bounds__(kDecodeWaves * 64, PAGED ? kWgPerCu : 1) void decode_kernel(
+    DecodeArgs a, float *out) {
     constexpr int DB = D / 16;   // 16-wide output blocks
     __shared__ int32_t sOff[kPlanItems + 1];
     __shared__ int32_t sWave[kDecodeWaves];
@@ -686,17 +687,22 @@ bool flat_plan(const reef_decode_params *p) {
     return items <= kPlanItems && items * ceil_div(p->max_context, kBlockKeys) < (int64_t(1) << 31);
 }
 
-// Workgroups of the launch: two per compute unit (8 waves, each with 16 KB of
-// cache in flight, keep HBM busy), or one per unit of work when there are fewer
-// (a workgroup that takes several items in turn pays each item's start-up and
-// merge latency once more: 128 one-block items took 66 us on 8 workgroups, 8 us
-// on 128). num_splits > 0 asks for that many waves per item on average instead.
-// Measured on MI355X at 128 x 8q/1kv ragged paged and 64 x 8kv x 4096 contiguous.
-int64_t decode_wgs(const reef_decode_params *p) {
+// Workgroups of the launch. A paged cache: two per compute unit (8 waves, each
+// with 16 KB of cache in flight: the 2 KB pages scatter the loads, and the second
+// workgroup's requests keep HBM busy). A contiguous cache streams at full bandwidth
+// with one per compute unit (one wave per SIMD); a second one only adds an
+// imbalance, its waves' loads being served behind the older workgroup's (its runs
+// ended up to 20 % later), and one per unit measured 6 % faster at 64 x 8kv x 4096
+// (the paged 128 x 8q/1kv ragged workload 2 % slower). Either way at most one per
+// unit of work (a workgroup that takes several items in turn pays each item's
+// start-up and merge latency once more: 128 one-block items took 66 us on 8
+// workgroups, 8 us on 128). num_splits > 0 asks for that many waves per item on
+// average instead.
+int64_t decode_wgs(const reef_decode_params *p, bool paged) {
     const int64_t items = p->batch * p->kv_heads;
     const int64_t units = flat_plan(p) ? items * ceil_div(p->max_context, kBlockKeys) : items;
     const int64_t g = p->num_splits > 0 ? ceil_div(items * p->num_splits, kDecodeWaves)
-                                        : kWgPerCu * compute_units();
+                                        : (paged ? kWgPerCu : 1) * compute_units();
     return std::max<int64_t>(1, std::min<int64_t>(std::min(g, units), 1 << 20));
 }
 
@@ -736,7 +742,8 @@ int64_t counter_bytes(const reef_decode_params *p) {
 
 int64_t workspace_bytes(const reef_decode_params *p) {
     const int64_t slot = (p->head_dim == 128 ? DecodeSlot<128>::ELEMS : DecodeSlot<64>::ELEMS) * 8;
-    return counter_bytes(p) + (flat_plan(p) ? decode_wgs(p) * 2 * slot : 0);
+    // Sized for the larger (paged) launch, so that one workspace serves both forms.
+    return counter_bytes(p) + (flat_plan(p) ? decode_wgs(p, true) * 2 * slot : 0);
 }
 
 template <bool PAGED>
@@ -752,7 +759,7 @@ reef_status launch_decode(const reef_decode_params *p, DecodeArgs &a, float *out
     a.score_scale = p->softmax_scale * kLog2e;
     a.items = (int32_t)(p->batch * p->kv_heads);
     a.flat = flat_plan(p) ? 1 : 0;
-    a.wgs = (int32_t)decode_wgs(p);
+    a.wgs = (int32_t)decode_wgs(p, PAGED);
     a.counters = static_cast<uint32_t *>(workspace);
     a.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + counter_bytes(p));
     const dim3 grid((unsigned)a.wgs);
