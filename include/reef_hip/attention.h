@@ -342,6 +342,34 @@ reef_status reef_kv_append_int8_paged(const reef_kv_append_params *p, const floa
                                       float *v_scale_pages, int32_t *context_lens,
                                       uint32_t *status_word, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Prefill over the int8 cache (chunked and multi-turn prompts): Attention::forward
+ * with query_len > 1 on a cache that already holds the chunk's keys and values
+ * (the engine appends first, then runs context() over every cached key with
+ * query_start = key_len - query_len, attention.hpp:354-372 and :415). The cache is
+ * the decode format above: contiguous when block_table is NULL (k_cache
+ * [B, Hkv, max_context, D], v_cache [B, Hkv, max_context/16, D, 16], scales
+ * [B, Hkv, max_context]), paged otherwise (k_cache [P, Hkv, 16, D], v_cache
+ * [P, Hkv, D, 16], scales [P, Hkv, 16], block_table [B, max_blocks_per_seq],
+ * P = num_pages; max_context is not used). p->kv_len is the number of cached
+ * tokens of every sequence (the chunk's included), p->q_len the chunk length,
+ * p->query_start normally kv_len - q_len; p->kv_granularity must be
+ * REEF_SCALE_PER_TOKEN (the cache's scales). q, q_scales, out and out_strides are
+ * as for reef_attention_prefill_int8. The call gathers the kv_len cached tokens of
+ * every (sequence, kv head) into token-major rows in the workspace (at least
+ * reef_attention_prefill_cache_workspace_bytes(p) bytes, 256-byte aligned, no
+ * zero-fill needed) and runs the prefill attention over them. A page number
+ * outside [0, num_pages) sets BAD_PAGE in status_word (optional) and reads as
+ * zero codes. */
+size_t reef_attention_prefill_cache_workspace_bytes(const reef_attention_params *p);
+
+reef_status reef_attention_prefill_int8_cache(
+    const reef_attention_params *p, const int8_t *q, const reef_strides *q_strides,
+    const float *q_scales, const int8_t *k_cache, const int8_t *v_cache, const float *k_scales,
+    const float *v_scales, int64_t max_context, const int32_t *block_table,
+    int64_t max_blocks_per_seq, int64_t num_pages, float *out, const reef_strides *out_strides,
+    void *workspace, size_t workspace_bytes, uint32_t *status_word, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

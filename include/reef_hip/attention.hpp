@@ -117,6 +117,29 @@ inline void context(const reef_attention_params &p, const int8_t *q, const reef_
           "attention context");
 }
 
+// Attention::forward with query_len > 1 on a non-empty cache (attention.hpp:354-372):
+// the chunk's keys are already in the int8 cache (append_kv_cache); the chunk's
+// queries attend over all p.kv_len cached keys. block_table nullptr: contiguous
+// cache of max_context tokens per sequence; otherwise paged. The caller owns the
+// workspace (prefill_cache_workspace_bytes(p) bytes).
+inline size_t prefill_cache_workspace_bytes(const reef_attention_params &p) {
+    return reef_attention_prefill_cache_workspace_bytes(&p);
+}
+
+inline void context_cache(const reef_attention_params &p, const int8_t *q,
+                          const reef_strides *q_strides, const float *q_scales,
+                          const int8_t *k_cache, const int8_t *v_cache, const float *k_scales,
+                          const float *v_scales, int64_t max_context, const int32_t *block_table,
+                          int64_t max_blocks_per_seq, int64_t num_pages, float *out,
+                          const reef_strides *out_strides, void *workspace,
+                          size_t workspace_bytes, uint32_t *status_word, hipStream_t stream) {
+    check(reef_attention_prefill_int8_cache(&p, q, q_strides, q_scales, k_cache, v_cache,
+                                            k_scales, v_scales, max_context, block_table,
+                                            max_blocks_per_seq, num_pages, out, out_strides,
+                                            workspace, workspace_bytes, status_word, stream),
+          "attention context over the cache");
+}
+
 // One decode step over a contiguous int8 cache. The caller owns the workspace
 // (decode_workspace_bytes(p) bytes); see attention.h for the cache layout.
 inline size_t decode_workspace_bytes(const reef_decode_params &p) {

@@ -8,7 +8,8 @@
 //        Attention::context (:374-432), which for the device model is the
 //        specialization below: the new key and value rows go into a device int8
 //        cache (reef_hip::append_kv_cache), and a prompt is attended with
-//        reef_hip::context (int8 prefill kernel) or one token with
+//        reef_hip::context (int8 prefill kernel), a later chunk of a prompt with
+//        reef_hip::context_cache (the prefill over the cache) or one token with
 //        reef_hip::decode (int8 decode kernel over the cache). Layer kind
 //        (GlobalAttention or LocalAttention and its window) comes from the
 //        engine's own visibility policy.
@@ -32,8 +33,12 @@
 //      unscaled scores (attention.hpp:104); the bound is the engine's own for its
 //      W8A8 model (test_gpt_neo.cpp:167-187), under kModelFrac of the largest
 //      logit.
-//   4. greedy generation of kGenerate tokens, reported.
-// Exit status 0 when checks 1-3 pass. Built by `make -C oracle gpt_neo` into
+//   4. a prompt fed in chunks: the later chunks attend over the earlier chunks'
+//      cached keys through reef_hip::context_cache (the prefill over the device
+//      cache); the logits after every chunk against those of one token at a time,
+//      max |diff| <= kPrefillDecodeTol;
+//   5. greedy generation of kGenerate tokens, reported.
+// Exit status 0 when checks 1-4 pass. Built by `make -C oracle gpt_neo` into
 // oracle/_ref/ (it needs the engine headers); run on a machine with a GPU.
 #include <hip/hip_runtime.h>
 
@@ -81,18 +86,18 @@ struct DeviceLayer {
     float *qf = nullptr, *kf = nullptr, *vf = nullptr, *out = nullptr;  // [H, cap, D]
     int8_t *q8 = nullptr, *k8 = nullptr, *v8 = nullptr;                 // [H * cap, D]
     float *qs = nullptr, *ks8 = nullptr, *vs8 = nullptr;                // [H * cap]
-    void *pws = nullptr, *dws = nullptr;
-    size_t pws_bytes = 0, dws_bytes = 0;
+    void *pws = nullptr, *dws = nullptr, *cws = nullptr;
+    size_t pws_bytes = 0, dws_bytes = 0, cws_bytes = 0;
     uint32_t *status = nullptr;
 };
 
 hipStream_t g_stream = nullptr;
 int64_t g_capacity = 0;
 std::map<const void *, std::unique_ptr<DeviceLayer>> g_layers;
-long g_prefill_calls = 0, g_decode_calls = 0;
+long g_prefill_calls = 0, g_decode_calls = 0, g_chunk_calls = 0;
 // Largest |device - engine int8 composition| of an attention call, per call kind
 // (0 prefill, 1 decode) and layer kind (0 global, 1 local).
-double g_att_err[2][2] = {{0, 0}, {0, 0}};
+double g_att_err[3][2] = {{0, 0}, {0, 0}, {0, 0}};  // [prompt, decode, chunk][global, local]
 
 DeviceLayer &layer_for(const void *attention, int64_t heads, int64_t dim) {
     auto &slot = g_layers[attention];
@@ -127,6 +132,8 @@ DeviceLayer &layer_for(const void *attention, int64_t heads, int64_t dim) {
             L->pws = dev_alloc<uint8_t>(L->pws_bytes);
             hip_ok(hipMemset(L->pws, 0, L->pws_bytes), "hipMemset");
         }
+        L->cws_bytes = reef_hip::prefill_cache_workspace_bytes(pp);
+        L->cws = dev_alloc<uint8_t>(L->cws_bytes);
         reef_decode_params dp{1, heads, heads, dim, g_capacity, 0, 1.0f, REEF_SCALE_PER_TOKEN, 0, 0};
         L->dws_bytes = reef_hip::decode_workspace_bytes(dp);
         L->dws = dev_alloc<uint8_t>(L->dws_bytes);
@@ -183,11 +190,18 @@ Tensor<double> Attention<double>::context(const Qkv<double> &qkv) const {
                          L.status, s);
         reef_hip::check_status_word(L.status, s, "decode");
         ++g_decode_calls;
+    } else if (start > 0) {
+        // A later chunk of a prompt (or a multi-token turn): its queries attend over
+        // every cached position, read from the device cache.
+        const reef_attention_params p{1, H, H, q_len, key_len, D, start, window, 1.0f,
+                                      REEF_SCALE_PER_TOKEN, REEF_SCALE_PER_TOKEN, 0};
+        reef_hip::context_cache(p, L.q8, nullptr, L.qs, L.k, L.v, L.ks, L.vs, L.cap, nullptr, 0,
+                                0, L.out, nullptr, L.cws, L.cws_bytes, L.status, s);
+        reef_hip::check_status_word(L.status, s, "context_cache");
+        ++g_chunk_calls;
     } else {
         // A prompt: the prefill kernel attends it from its own int8 rows (token-major
         // values), the same codes the cache holds.
-        if (start != 0)
-            throw reef_hip::unsupported("prefill on top of cached positions (chunked prefill)");
         reef_hip::quantize_rows(L.kf, H * q_len, D, D, L.k8, L.ks8, L.status, s);
         reef_hip::quantize_rows(L.vf, H * q_len, D, D, L.v8, L.vs8, L.status, s);
         const reef_attention_params p{1, H, H, q_len, q_len, D, 0, window, 1.0f,
@@ -233,7 +247,7 @@ Tensor<double> Attention<double>::context(const Qkv<double> &qkv) const {
             err = std::max(err, std::fabs((double)ref.values[i] -
                                           mixed.values[h * ref.values.size() + i]));
     }
-    double &slot = g_att_err[q_len == 1 ? 1 : 0][window > 0 ? 1 : 0];
+    double &slot = g_att_err[q_len == 1 ? 1 : start > 0 ? 2 : 0][window > 0 ? 1 : 0];
     slot = std::max(slot, err);
     return mixed;
 }
@@ -317,6 +331,22 @@ int main() {
                 m.forward(ie::TokenIds(prompt.begin(), prompt.begin() + (std::ptrdiff_t)len));
             pd = std::max(pd, max_diff(pre, stepped[len - 1]));
         }
+        // 1b. a prompt fed in chunks (the later chunks attend over the cached keys of
+        // the earlier ones, from the device cache) == the whole prompt == one token at
+        // a time, after every chunk.
+        const std::vector<std::vector<size_t>> schedules = {
+            {17, 13, 10}, {1, 39}, {39, 1}, {20, 20}, {2, 3, 5, 7, 11, 12}, {25, 1, 14}};
+        double pc = 0.0;
+        for (const auto &chunks : schedules) {
+            ie::GPTNeo<double> m(wd);
+            size_t at = 0;
+            for (size_t n : chunks) {
+                const ie::Tensor<double> out = m.forward(ie::TokenIds(
+                    prompt.begin() + (std::ptrdiff_t)at, prompt.begin() + (std::ptrdiff_t)(at + n)));
+                at += n;
+                pc = std::max(pc, max_diff(out, stepped[at - 1]));
+            }
+        }
         // 2. the device model against the engine's float model, prompt logits.
         ie::GPTNeo<float> engine(wf);
         ie::GPTNeo<double> device(wd);
@@ -331,27 +361,36 @@ int main() {
         size_t same = 0;
         while (same < kGenerate && ge[same] == gd[same]) ++same;
 
-        const double call_err = std::max(std::max(g_att_err[0][0], g_att_err[0][1]),
-                                         std::max(g_att_err[1][0], g_att_err[1][1]));
+        double call_err = 0.0;
+        for (const auto &row : g_att_err) call_err = std::max(call_err, std::max(row[0], row[1]));
         const bool ok1 = call_err <= kCallTol, ok2 = pd <= kPrefillDecodeTol,
-                   ok3 = de <= kModelFrac * scale;
+                   ok3 = de <= kModelFrac * scale, ok4 = pc <= kPrefillDecodeTol;
         std::printf("%s every attention call vs the engine's int8 composition, max |diff| %.3e "
-                    "(bound %.0e): prefill global %.3e local %.3e, decode global %.3e local %.3e\n",
+                    "(bound %.0e): prompt global %.3e local %.3e, decode global %.3e local %.3e, "
+                    "later chunk global %.3e local %.3e\n",
                     ok1 ? "ok  " : "FAIL", call_err, kCallTol, g_att_err[0][0], g_att_err[0][1],
-                    g_att_err[1][0], g_att_err[1][1]);
+                    g_att_err[1][0], g_att_err[1][1], g_att_err[2][0], g_att_err[2][1]);
         std::printf("%s prefill == decode (40 prompt lengths), max |dlogit| %.3e (bound %.0e)\n",
                     ok2 ? "ok  " : "FAIL", pd, kPrefillDecodeTol);
+        std::printf("%s chunked prompt == one token at a time (%zu chunk schedules), max |dlogit| "
+                    "%.3e (bound %.0e)\n", ok4 ? "ok  " : "FAIL", schedules.size(), pc,
+                    kPrefillDecodeTol);
         std::printf("%s device vs engine float model, max |dlogit| %.3e (bound %.3e)\n",
                     ok3 ? "ok  " : "FAIL", de, kModelFrac * scale);
         std::printf("info greedy %zu tokens: first %zu identical to the engine's\n", kGenerate,
                     same);
-        std::printf("info device calls: %ld prefill, %ld decode\n", g_prefill_calls,
-                    g_decode_calls);
+        std::printf("info device calls: %ld prefill, %ld decode, %ld later-chunk\n",
+                    g_prefill_calls, g_decode_calls, g_chunk_calls);
         std::printf("{\"call_max_diff\": %.6e, \"prefill_decode_max_diff\": %.6e, "
+                    "\"chunked_max_diff\": %.6e, "
                     "\"engine_max_diff\": %.6e, \"max_logit\": %.6e, \"greedy_same_prefix\": %zu, "
-                    "\"prefill_calls\": %ld, \"decode_calls\": %ld}\n", call_err, pd, de, scale,
-                    same, g_prefill_calls, g_decode_calls);
-        return ok1 && ok2 && ok3 && g_prefill_calls > 0 && g_decode_calls > 0 ? 0 : 1;
+                    "\"prefill_calls\": %ld, \"decode_calls\": %ld, \"chunk_calls\": %ld}\n",
+                    call_err, pd, pc, de, scale, same, g_prefill_calls, g_decode_calls,
+                    g_chunk_calls);
+        return ok1 && ok2 && ok3 && ok4 && g_prefill_calls > 0 && g_decode_calls > 0 &&
+                       g_chunk_calls > 0
+                   ? 0
+                   : 1;
     } catch (const std::exception &e) {
         std::printf("FAIL exception: %s\n", e.what());
         return 2;

@@ -37,7 +37,8 @@ EXPORTS = [
     "reef_attention_decode_int8_paged", "reef_attention_decode_int8_paged_noalloc",
     "reef_kv_pack_v_pages", "reef_kv_append_int8",
     "reef_kv_append_int8_paged", "reef_attention_int8_integer", "reef_linear_w8a8_workspace_bytes",
-    "reef_linear_w8a8", "reef_gemm_w8a8",
+    "reef_linear_w8a8", "reef_gemm_w8a8", "reef_attention_prefill_cache_workspace_bytes",
+    "reef_attention_prefill_int8_cache",
 ]
 
 
@@ -132,6 +133,10 @@ _SIGS = {
     "reef_kv_append_int8_paged": [C.POINTER(KvAppendParams), _P, C.POINTER(Strides), _P,
                                   C.POINTER(Strides), _P, _P, _I64, _I64, _P, _P, _P, _P, _P,
                                   _P, _P],
+    "reef_attention_prefill_cache_workspace_bytes": [C.POINTER(AttentionParams)],
+    "reef_attention_prefill_int8_cache": [C.POINTER(AttentionParams), _P, C.POINTER(Strides), _P,
+                                          _P, _P, _P, _P, _I64, _P, _I64, _I64, _P,
+                                          C.POINTER(Strides), _P, C.c_size_t, _P, _P],
 }
 
 _lib_handle = None
@@ -327,6 +332,46 @@ def attention_prefill(q, k, v, q_scales, k_scales, v_scales, *, query_start=None
         C.byref(p), _ptr(q), C.byref(qs), _ptr(k), C.byref(ks), _ptr(v), C.byref(vs),
         _ptr(q_scales.contiguous()), _ptr(k_scales.contiguous()), _ptr(v_scales.contiguous()),
         _ptr(out), C.byref(os_), ws_ptr, ws_n, _stream()), "attention_prefill")
+    return out
+
+
+def attention_prefill_cache(q, q_scales, k_cache, v_cache, k_scales, v_scales, kv_len, *,
+                            block_table=None, query_start=None, window=0, softmax_scale=None,
+                            q_granularity=PER_HEAD, status: StatusWord | None = None, out=None):
+    """A prompt chunk over the int8 cache (Attention::forward with query_len > 1 on a
+    non-empty cache, attention.hpp:354-372): the cache already holds the chunk's
+    keys (kv_append), kv_len tokens per sequence. Contiguous cache (block_table
+    None): k_cache [B, Hkv, L, D], v_cache [B, Hkv, L/16, D, 16] (or the same bytes
+    in any shape), scales [B, Hkv, L]. Paged: k_cache [P, Hkv, 16, D], v_cache
+    [P, Hkv, D, 16], scales [P, Hkv, 16], block_table [B, max_blocks] int32.
+    q [B, Hq, q_len, D] int8; returns fp32 [B, Hq, q_len, D]."""
+    torch = _torch()
+    _require(q, torch.int8, "q")
+    B, Hq, Sq, D = q.shape
+    Hkv = k_cache.shape[1]
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    start = kv_len - Sq if query_start is None else query_start
+    p = AttentionParams(B, Hq, Hkv, Sq, kv_len, D, start, window, softmax_scale, q_granularity,
+                        PER_TOKEN, 0)
+    if block_table is None:
+        max_context, table, max_blocks, pages = k_cache.shape[2], None, 0, 0
+    else:
+        max_context, table = 0, block_table.contiguous()
+        max_blocks, pages = table.shape[1], k_cache.shape[0]
+    n = lib().reef_attention_prefill_cache_workspace_bytes(C.byref(p))
+    ws = torch.empty(max(n, 256), dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty((B, Hq, Sq, D), dtype=torch.float32, device=q.device)
+    qs, os_ = _strides4(q), _strides4(out)
+    own = status or StatusWord(q.device)
+    check(lib().reef_attention_prefill_int8_cache(
+        C.byref(p), _ptr(q), C.byref(qs), _ptr(q_scales.contiguous()), _ptr(k_cache.contiguous()),
+        _ptr(v_cache.contiguous()), _ptr(k_scales.contiguous()), _ptr(v_scales.contiguous()),
+        max_context, _ptr(table), max_blocks, pages, _ptr(out), C.byref(os_), _ptr(ws), n,
+        own.ptr, _stream()), "attention_prefill_cache")
+    if status is None:
+        own.check("attention_prefill_cache")
     return out
 
 

@@ -11,8 +11,8 @@ import sys
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
-SOURCES = ["quant.hip", "prefill.hip", "prefill_packed.hip", "decode.hip", "kv_append.hip",
-           "int_head.hip", "linear.hip"]
+SOURCES = ["quant.hip", "prefill.hip", "prefill_packed.hip", "prefill_cache.hip", "decode.hip",
+           "kv_append.hip", "int_head.hip", "linear.hip"]
 LIB = os.path.join(PKG, "libreef_hip.so")
 
 FLAGS = [

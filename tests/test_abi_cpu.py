@@ -93,6 +93,34 @@ def test_prefill_workspace_bytes_and_alignment():
                                            C.c_void_p(0x10010), n, None) == reef_amd.INVALID_ARGUMENT
 
 
+def _prefill_cache(p, ws_bytes=1 << 30, max_context=64, table=None, max_blocks=0, pages=0):
+    lib = reef_amd.lib()
+    return lib.reef_attention_prefill_int8_cache(
+        C.byref(p), _fake(1), None, _fake(2), _fake(3), _fake(4), _fake(5), _fake(6), max_context,
+        table, max_blocks, pages, _fake(7), None, _fake(8), ws_bytes, None, None)
+
+
+def test_prefill_cache_host_validation_and_workspace():
+    """The prefill over the decode cache: gathered rows and per-token scales in the
+    workspace, arguments checked before any launch."""
+    lib = reef_amd.lib()
+    tok = dict(kv_granularity=2, q_len=8, kv_len=40, query_start=32)
+    p = good_params(**tok)
+    # 1 x 2 kv heads x 40 tokens: keys and values (80 rows x 128 bytes, rounded to
+    # 256), then two scale arrays (80 floats, rounded to 256)
+    assert lib.reef_attention_prefill_cache_workspace_bytes(C.byref(p)) == 2 * 10240 + 2 * 512
+    assert lib.reef_attention_prefill_cache_workspace_bytes(C.byref(good_params(head_dim=96))) == 0
+    assert _prefill_cache(good_params(**dict(tok, kv_granularity=1))) == reef_amd.INVALID_ARGUMENT
+    assert _prefill_cache(good_params(**dict(tok, query_start=33))) == reef_amd.INVALID_ARGUMENT
+    assert _prefill_cache(p, max_context=32) == reef_amd.INVALID_ARGUMENT  # cache shorter than kv_len
+    assert _prefill_cache(p, max_context=72) == reef_amd.INVALID_ARGUMENT  # not a multiple of 16
+    assert _prefill_cache(p, ws_bytes=1000) == reef_amd.INVALID_ARGUMENT
+    assert _prefill_cache(good_params(**dict(tok, head_dim=96))) == reef_amd.UNSUPPORTED
+    # paged: the block table must cover kv_len and the pool must be non-empty
+    assert _prefill_cache(p, table=_fake(9), max_blocks=2, pages=10) == reef_amd.INVALID_ARGUMENT
+    assert _prefill_cache(p, table=_fake(9), max_blocks=3, pages=0) == reef_amd.INVALID_ARGUMENT
+
+
 def test_decode_host_validation_and_workspace():
     lib = reef_amd.lib()
     p = DecodeParams(batch=64, q_heads=32, kv_heads=8, head_dim=128, max_context=4096,
