@@ -422,6 +422,38 @@ def bench_extras(torch, reef, W, steps):
     out["kv_append"] = {"workload": f"{T}-token chunk, {B} sequences x {H} KV heads, d {D}",
                         "ms": round(ap_ms, 5), "GB/s": round(ab / (ap_ms * 1e-3) / 1e9, 1),
                         "frac_hbm": round(ab / (ap_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    del kf, vf, kc, vc, kcs, vcs
+    # prefill over the cache: a 512-token turn of one sequence, 8 q / 1 KV head, on a
+    # paged cache that holds 4096 tokens (the turn's included)
+    Hq, Hkv, S, KV = 8, 1, 512, 4096
+    pool = KV // 16 + 64
+    kp = torch.randint(-127, 128, (pool, Hkv, 16, D), dtype=torch.int8, device="cuda", generator=g)
+    vp = torch.randint(-127, 128, (pool, Hkv, D, 16), dtype=torch.int8, device="cuda", generator=g)
+    ksp = torch.rand((pool, Hkv, 16), device="cuda", generator=g) * 0.01 + 0.01
+    vsp = torch.rand((pool, Hkv, 16), device="cuda", generator=g) * 0.01 + 0.01
+    table = torch.randperm(pool, device="cuda", generator=g)[: KV // 16].to(torch.int32)[None]
+    qc = torch.randint(-127, 128, (1, Hq, S, D), dtype=torch.int8, device="cuda", generator=g)
+    qcs = torch.rand(Hq, device="cuda", generator=g) * 0.01 + 0.01
+    cp = reef.AttentionParams(1, Hq, Hkv, S, KV, D, KV - S, 0, 1 / math.sqrt(D), reef.PER_HEAD,
+                              reef.PER_TOKEN, 0)
+    cws_n = lib.reef_attention_prefill_cache_workspace_bytes(C.byref(cp))
+    cws = torch.zeros(cws_n, dtype=torch.uint8, device="cuda")
+    yc = torch.empty((1, Hq, S, D), device="cuda")
+    qst, yst = reef.Strides(*qc.stride()[:3]), reef.Strides(*yc.stride()[:3])
+
+    def chunk():
+        rc = lib.reef_attention_prefill_int8_cache(
+            C.byref(cp), P(qc), C.byref(qst), P(qcs), P(kp), P(vp), P(ksp), P(vsp), 0, P(table),
+            table.shape[1], pool, P(yc), C.byref(yst), P(cws), cws_n, None, st())
+        if rc != 0:
+            raise RuntimeError(f"prefill over the cache status {rc}")
+    _, ch_ms = timed(torch, chunk, steps, 3)
+    pairs = S * (KV - S) + S * (S + 1) // 2
+    cops = 4 * D * pairs * Hq
+    out["prefill_over_cache"] = {
+        "workload": f"{S}-token turn over a {KV}-token paged cache, {Hq}q/{Hkv}kv, d {D}",
+        "ms": round(ch_ms, 5), "TOPS": round(cops / (ch_ms * 1e-3) / 1e12, 1),
+        "note": "gather of the cached pages + prefill with per-token K/V scales (hi + lo P)"}
     return out
 
 

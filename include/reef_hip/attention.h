@@ -146,15 +146,19 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
 /* Prefill work schedule (bits 4-6 of flags). AUTO lets the library choose from the
  * grid size and the workspace; the others force one schedule, for callers that
  * tune it and for tests that must reach every path. A forced schedule that the
- * call cannot use (BALANCED without a large enough workspace, or with PRECISE_PV or
- * PER_TOKEN K/V scales) returns REEF_INVALID_ARGUMENT. */
+ * call cannot use (BALANCED without a large enough workspace, SPLIT with PRECISE_PV
+ * or PER_TOKEN K/V scales, PACKED without head_dim 128, per-tensor or per-head K/V
+ * scales and a workspace) returns REEF_INVALID_ARGUMENT. AUTO takes BALANCED for a
+ * call with PRECISE_PV or PER_TOKEN K/V scales, a large enough workspace and fewer
+ * 128-row query tiles than compute units. */
 #define REEF_ATTN_SCHED_MASK 0x70u
 #define REEF_ATTN_SCHED_AUTO 0x00u
 #define REEF_ATTN_SCHED_ONE_ITEM 0x10u /* one 128-row query tile per workgroup */
 #define REEF_ATTN_SCHED_SPLIT 0x20u    /* persistent workgroups; two 4-wave groups split
                                         * each tile's keys */
 #define REEF_ATTN_SCHED_BALANCED 0x30u /* equal (tile, key block) ranges per workgroup;
-                                        * cut tiles merge through the workspace */
+                                        * cut tiles merge through the workspace; hi + lo
+                                        * P with PRECISE_PV or PER_TOKEN K/V scales */
 #define REEF_ATTN_SCHED_PACKED 0x40u   /* head_dim 128, per-tensor / per-head K and V
                                         * scales: V packed once into an fp16 image in the
                                         * workspace, 256-row query tiles, persistent
@@ -180,11 +184,14 @@ typedef struct reef_attention_params {
  *
  * workspace (optional, 256-byte aligned, at least
  * reef_attention_prefill_workspace_bytes(p) bytes; NULL/0 allowed) holds the
- * counters and partial results of the balanced schedule and, for head_dim 128, the
- * fp16 value image of the packed schedule (2 bytes per V element). It must be
- * zero-filled before its first use; every call leaves the counters zero-filled.
- * Without it the library uses the schedules that need none. Calls that may run at
- * the same time need separate workspaces. */
+ * counters (a fixed 256 KB region, at most 65536 items of 128 query rows) and
+ * partial results of the balanced schedule and, for head_dim 128, the fp16 value
+ * image of the packed schedule (2 bytes per V element). It must be zero-filled
+ * before its first use; every call leaves the counters zero-filled, and the
+ * counters sit at the same offsets for every shape, so one workspace serves calls
+ * of any shape that it is large enough for. Without it the library uses the
+ * schedules that need none. Calls that may run at the same time need separate
+ * workspaces. */
 size_t reef_attention_prefill_workspace_bytes(const reef_attention_params *p);
 
 reef_status reef_attention_prefill_int8(const reef_attention_params *p, const int8_t *q,
@@ -257,12 +264,13 @@ typedef struct reef_decode_params {
 /* Bytes of device workspace the decode entry points need for params. The launch
  * deals the keys of all (sequence, kv head) items out to its workgroups in equal
  * runs of 64-key blocks, whatever the context lengths (with at most 2048 items;
- * beyond that, in equal runs of whole items). The workspace holds one counter per
- * item and two partial-result slots per workgroup; an item whose keys span several
- * workgroups is merged by the last of them inside the same launch. The workspace
- * must be zero-filled before its first use; every call leaves it ready for the
- * next (no refill). Calls that may run at the same time need separate
- * workspaces. */
+ * beyond that, in equal runs of whole items). The workspace holds a fixed 8 KB
+ * region of counters (one per item, at the same offset for every shape) and two
+ * partial-result slots per workgroup; an item whose keys span several workgroups
+ * is merged by the last of them inside the same launch. The workspace must be
+ * zero-filled before its first use; every call leaves it ready for the next call of
+ * any shape it is large enough for (no refill). Calls that may run at the same
+ * time need separate workspaces. */
 size_t reef_attention_decode_workspace_bytes(const reef_decode_params *p);
 
 reef_status reef_attention_decode_int8(const reef_decode_params *p, const int8_t *q,
@@ -357,10 +365,11 @@ reef_status reef_kv_append_int8_paged(const reef_kv_append_params *p, const floa
  * REEF_SCALE_PER_TOKEN (the cache's scales). q, q_scales, out and out_strides are
  * as for reef_attention_prefill_int8. The call gathers the kv_len cached tokens of
  * every (sequence, kv head) into token-major rows in the workspace (at least
- * reef_attention_prefill_cache_workspace_bytes(p) bytes, 256-byte aligned, no
- * zero-fill needed) and runs the prefill attention over them. A page number
- * outside [0, num_pages) sets BAD_PAGE in status_word (optional) and reads as
- * zero codes. */
+ * reef_attention_prefill_cache_workspace_bytes(p) bytes, 256-byte aligned; its
+ * first part is the prefill's balanced-schedule workspace, so it must be
+ * zero-filled before its first use, and every call leaves it ready for the next)
+ * and runs the prefill attention over them. A page number outside [0, num_pages)
+ * sets BAD_PAGE in status_word (optional) and reads as zero codes. */
 size_t reef_attention_prefill_cache_workspace_bytes(const reef_attention_params *p);
 
 reef_status reef_attention_prefill_int8_cache(

@@ -134,6 +134,7 @@ DeviceLayer &layer_for(const void *attention, int64_t heads, int64_t dim) {
         }
         L->cws_bytes = reef_hip::prefill_cache_workspace_bytes(pp);
         L->cws = dev_alloc<uint8_t>(L->cws_bytes);
+        hip_ok(hipMemset(L->cws, 0, L->cws_bytes), "hipMemset");
         reef_decode_params dp{1, heads, heads, dim, g_capacity, 0, 1.0f, REEF_SCALE_PER_TOKEN, 0, 0};
         L->dws_bytes = reef_hip::decode_workspace_bytes(dp);
         L->dws = dev_alloc<uint8_t>(L->dws_bytes);

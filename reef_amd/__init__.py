@@ -360,7 +360,11 @@ def attention_prefill_cache(q, q_scales, k_cache, v_cache, k_scales, v_scales, k
         max_context, table = 0, block_table.contiguous()
         max_blocks, pages = table.shape[1], k_cache.shape[0]
     n = lib().reef_attention_prefill_cache_workspace_bytes(C.byref(p))
-    ws = torch.empty(max(n, 256), dtype=torch.uint8, device=q.device)
+    key = ("cache", torch.device(q.device).index, _stream().value)
+    ws = _PREFILL_WS.get(key)
+    if ws is None or ws.numel() < n:  # zero-filled once; every call leaves it so
+        ws = torch.zeros(max(n, 256), dtype=torch.uint8, device=q.device)
+        _PREFILL_WS[key] = ws
     if out is None:
         out = torch.empty((B, Hq, Sq, D), dtype=torch.float32, device=q.device)
     qs, os_ = _strides4(q), _strides4(out)

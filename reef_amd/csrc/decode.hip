@@ -734,11 +734,16 @@ reef_status validate(const reef_decode_params *p, const int8_t *q, const float *
     return REEF_OK;
 }
 
-// Workspace: one counter per (sequence, kv head), then, when blocks are dealt
-// out, two part slots per workgroup (the first and the last segment of its run).
-int64_t counter_bytes(const reef_decode_params *p) {
-    return ceil_div(p->batch * p->kv_heads * 4, 256) * 256;
-}
+// Workspace: a fixed region of kPlanItems counters (one per (sequence, kv head);
+// only a launch that deals out blocks, with at most kPlanItems items, counts
+// parts), then, for such a launch, two part slots per workgroup (the first and
+// the last segment of its run). Counter i sits at the same place whatever the
+// shape of the call, and every launch leaves the counters it used at zero, so one
+// zero-filled workspace serves calls of any shape; the slots are written before
+// they are read.
+constexpr int64_t kCounterBytes = kPlanItems * 4;
+
+int64_t counter_bytes(const reef_decode_params *) { return kCounterBytes; }
 
 int64_t workspace_bytes(const reef_decode_params *p) {
     const int64_t slot = (p->head_dim == 128 ? DecodeSlot<128>::ELEMS : DecodeSlot<64>::ELEMS) * 8;

@@ -80,7 +80,6 @@ struct StreamPart {
     int slot;       // this part's slot
     int item;       // counter index
     int first_wg;   // logical workgroup of the item's first part
-    int self;       // this part's index among the item's parts
     int64_t item_u0;  // first step of the item
 };
 
@@ -250,7 +249,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                                              const StreamArgs &sa, const StreamPart &sp,
                                              uint32_t *sTicket) {
     constexpr bool SPLIT = MODE == kSplit;
-    static_assert(MODE == kWhole || !KV_TOKEN, "only whole items have per-token K/V scales");
+    static_assert(MODE != kSplit || !KV_TOKEN, "the split kernel has no per-token K/V scales");
     constexpr int KSTRIDE = PrefillLds<D>::KSTRIDE, VSTRIDE = PrefillLds<D>::VSTRIDE;
     constexpr int DB = D / 32;  // 32-wide output blocks
     constexpr int K_BYTES = PrefillLds<D>::K_BYTES, V_BYTES = PrefillLds<D>::V_BYTES;
@@ -610,6 +609,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                 for (int i = 0; i < 4; ++i) acc[d][4 * j + i] = acc[d][4 * j + i] * w0 + o[i] * w1;
             }
     }
+    if (KV_TOKEN && MODE == kStream) {
+        // Parts merge in absolute value units: the accumulator leaves the units of
+        // s_run (the largest value scale this part saw) here.
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[d][i] *= s_run;
+        s_run = 1.0f;
+    }
     if (MODE == kStream && sp.parts > 1) {
         // Leave this part in its slot (every lane: rows past q_len hold finite
         // values), then count the part in; the last part of the item merges. The
@@ -657,44 +665,47 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             return reinterpret_cast<const uint64_t *>(sa.slots +
                                                       (int64_t)(2 * L + (second ? 1 : 0)) * SF);
         };
-        // This part comes from registers, the others from their slots, summed in
-        // part order either way with explicit fused multiply-adds (the same
-        // roundings whichever part merges).
-        float m = m_run;
-        for (int p = 0; p < sp.parts; ++p)
-            if (p != sp.self)
-                m = fmaxf(m, __uint_as_float((uint32_t)get(slot_of(p) + OF / 2 + wave * kWave + lane)));
-        float l = 0.0f;
+        // Every part, this one included, comes from its slot, folded in part order (a
+        // running log-sum-exp with explicit fused multiply-adds: the same roundings
+        // whichever part merges), kMergeAhead parts' loads in flight at a time.
+        constexpr int kMergeAhead = KV_TOKEN || PRECISE ? 2 : 1;
+        float m = -INFINITY, l = 0.0f;
         f32x16 tot[DB];
 #pragma unroll
         for (int d = 0; d < DB; ++d) tot[d] = f32x16{};
-        for (int p = 0; p < sp.parts; ++p) {
-            if (p == sp.self) {
-                const float w = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
-                l = __builtin_fmaf(w, l_tot, l);
-#pragma unroll
-                for (int d = 0; d < DB; ++d)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) tot[d][i] = __builtin_fmaf(w, acc[d][i], tot[d][i]);
-                continue;
-            }
-            const uint64_t *sl = slot_of(p);
-            const uint64_t ml = get(sl + OF / 2 + wave * kWave + lane);
-            uint64_t v[DB * 8];
-#pragma unroll
-            for (int e = 0; e < DB * 8; ++e) v[e] = get(sl + (wave * E + e) * kWave + lane);
-            const float mp = __uint_as_float((uint32_t)ml), lp = __uint_as_float((uint32_t)(ml >> 32));
-            const float w = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - m);
-            l = __builtin_fmaf(w, lp, l);
+        auto fold = [&](float mp, float lp, auto &&value) {
+            const float mn = fmaxf(m, mp);
+            const float er = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+            const float ep = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp - mn);
+            l = __builtin_fmaf(ep, lp, l * er);
 #pragma unroll
             for (int d = 0; d < DB; ++d)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    tot[d][2 * e] =
-                        __builtin_fmaf(w, __uint_as_float((uint32_t)v[d * 8 + e]), tot[d][2 * e]);
-                    tot[d][2 * e + 1] = __builtin_fmaf(
-                        w, __uint_as_float((uint32_t)(v[d * 8 + e] >> 32)), tot[d][2 * e + 1]);
-                }
+                for (int i = 0; i < 16; ++i)
+                    tot[d][i] = __builtin_fmaf(ep, value(d, i), tot[d][i] * er);
+            m = mn;
+        };
+        for (int p0 = 0; p0 < sp.parts; p0 += kMergeAhead) {
+            uint64_t ml[kMergeAhead], v[kMergeAhead][DB * 8];
+#pragma unroll
+            for (int j = 0; j < kMergeAhead; ++j) {
+                const int p = p0 + j;
+                if (p >= sp.parts) continue;
+                const uint64_t *sl = slot_of(p);
+                ml[j] = get(sl + OF / 2 + wave * kWave + lane);
+#pragma unroll
+                for (int e = 0; e < DB * 8; ++e) v[j][e] = get(sl + (wave * E + e) * kWave + lane);
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeAhead; ++j) {
+                const int p = p0 + j;
+                if (p >= sp.parts) continue;
+                fold(__uint_as_float((uint32_t)ml[j]), __uint_as_float((uint32_t)(ml[j] >> 32)),
+                     [&](int d, int i) {
+                         const uint64_t w = v[j][d * 8 + i / 2];
+                         return __uint_as_float((uint32_t)(i & 1 ? w >> 32 : w));
+                     });
+            }
         }
 #pragma unroll
         for (int d = 0; d < DB; ++d) acc[d] = tot[d];
@@ -761,10 +772,11 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
 // [L G^-1 units, (L + 1) G^-1 units) of logical workgroup L, where the G / 8
 // workgroups that run on one XCD (hardware workgroup g goes to XCD g % 8) hold
 // consecutive L, so an XCD's L2 sees a few heads, not all of them.
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void prefill_stream_kernel(PrefillArgs a, StreamArgs sa) {
+template <int D, bool KV_TOKEN, bool PRECISE>
+__global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_stream_kernel(
+    PrefillArgs a, StreamArgs sa) {
     __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
-    __shared__ float sScale[2][1];
+    __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
     __shared__ uint32_t sTicket;
     const int G = gridDim.x, g = blockIdx.x;
     const int x = g % kXcds, per = G / kXcds, rem = G % kXcds;
@@ -797,10 +809,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_stream_kernel(PrefillArgs
         sp.first_wg = wg_of(sp.item_u0);
         sp.parts = wg_of(sp.item_u0 + n - 1) - sp.first_wg + 1;
         sp.slot = 2 * L + (first ? 0 : 1);
-        sp.self = L - sp.first_wg;
         sp.item = bh * a.q_tiles + tile;
-        prefill_body<D, false, false, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0, c1,
-                                               smem, sScale, sa, sp, &sTicket);
+        prefill_body<D, KV_TOKEN, PRECISE, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0,
+                                                    c1, smem, sScale, sa, sp, &sTicket);
         u += c1 - c0;
         c0 = 0;
         first = false;
@@ -877,14 +888,20 @@ int64_t host_steps_before(const reef_attention_params &p, int64_t t) {
 // The balanced schedule's grid: two 4-wave workgroups per compute unit.
 int64_t stream_groups() { return 2 * compute_units(); }
 
-int64_t stream_counter_bytes(const reef_attention_params &p) {
-    const int64_t items = ceil_div(p.q_len, kBM) * p.q_heads * p.batch;
-    return ceil_div(items * 4, 256) * 256;
+// The balanced schedule's workspace layout is the same for every call: a fixed
+// region of counters (one per item, up to kStreamMaxItems items), then part slots
+// sized for head_dim 128. Counter i sits at the same place whatever the shape of
+// the call, and every launch leaves its counters at zero, so one zero-filled
+// workspace serves calls of any shape (the slots are written before they are read).
+constexpr int64_t kStreamMaxItems = 65536;
+constexpr int64_t kStreamMinSteps = 8;  // steps per workgroup of the precise balanced kernels
+constexpr int64_t kStreamCounterBytes = kStreamMaxItems * 4;
+
+int64_t stream_items(const reef_attention_params &p) {
+    return ceil_div(p.q_len, kBM) * p.q_heads * p.batch;
 }
 
-int64_t stream_slot_floats(int64_t D) {
-    return D == 128 ? StreamSlot<128>::FLOATS : StreamSlot<64>::FLOATS;
-}
+int64_t stream_slot_floats() { return StreamSlot<128>::FLOATS; }
 
 
 }  // namespace
@@ -896,9 +913,8 @@ namespace reef {
 namespace {
 // Workspace: the balanced schedule's counters and slots, then (head_dim 128) the
 // packed schedule's value image, 256-byte aligned.
-int64_t balanced_bytes(const reef_attention_params &p) {
-    return ceil_div(stream_counter_bytes(p) + 2 * stream_groups() * stream_slot_floats(p.head_dim) * 4,
-                    256) * 256;
+int64_t balanced_bytes(const reef_attention_params &) {
+    return ceil_div(kStreamCounterBytes + 2 * stream_groups() * stream_slot_floats() * 4, 256) * 256;
 }
 int64_t packed_bytes(const reef_attention_params &p) {
     return p.head_dim == 128 && p.kv_heads > 0 && p.kv_len > 0
@@ -913,6 +929,11 @@ bool packed_by_default(const reef_attention_params &p) {
     return pairs >= compute_units();
 }
 }  // namespace
+
+// The balanced schedule's workspace bytes (counters and part slots), for the
+// prefill over the cache.
+int64_t prefill_balanced_bytes(const reef_attention_params &p) { return balanced_bytes(p); }
+
 }  // namespace reef
 
 extern "C" size_t reef_attention_prefill_workspace_bytes(const reef_attention_params *p) {
@@ -1007,7 +1028,8 @@ extern "C" reef_status reef_attention_prefill_int8(
         sched != REEF_ATTN_SCHED_PACKED)
         return REEF_INVALID_ARGUMENT;
     const int64_t bal_bytes = balanced_bytes(*p);
-    const bool stream_ok = workspace && (int64_t)workspace_bytes >= bal_bytes;
+    const bool stream_ok = workspace && (int64_t)workspace_bytes >= bal_bytes &&
+                           stream_items(*p) <= kStreamMaxItems;
     const bool packed_ok = D == 128 && !tok && workspace &&
                            (int64_t)workspace_bytes >= bal_bytes + packed_bytes(*p);
     if (sched == REEF_ATTN_SCHED_PACKED && !packed_ok) return REEF_INVALID_ARGUMENT;
@@ -1018,29 +1040,50 @@ extern "C" reef_status reef_attention_prefill_int8(
         return prefill_packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out,
                                      ost, static_cast<char *>(workspace) + bal_bytes, stream);
     }
-    // The balanced and split schedules round P to one fp16 (11 bits); the library
-    // chooses them only when the caller forces them. The one-item kernel splits P
-    // into hi + lo where the values need it (per item, two launches).
-    if (sched == REEF_ATTN_SCHED_BALANCED && (tok || precise || !stream_ok))
-        return REEF_INVALID_ARGUMENT;
+    // The split schedule rounds P to one fp16 (11 bits); the balanced one takes P
+    // split into hi + lo when the call asks for precision (per-token K/V scales
+    // always do). Without a request for precision the library leaves both to callers
+    // that force them, and the one-item kernel splits P where the values need it (per
+    // item, two launches). With precision and fewer 128-row tiles than compute units
+    // (a short chunk of queries over a long cache), the library takes the balanced
+    // schedule: the one-item kernel would leave most of the GPU idle.
+    if (sched == REEF_ATTN_SCHED_BALANCED && !stream_ok) return REEF_INVALID_ARGUMENT;
     if (sched == REEF_ATTN_SCHED_SPLIT && (tok || precise)) return REEF_INVALID_ARGUMENT;
     a.item_sel = 0;
-    if (sched == REEF_ATTN_SCHED_BALANCED) {
+    if (sched == REEF_ATTN_SCHED_BALANCED ||
+        (sched == REEF_ATTN_SCHED_AUTO && precise && stream_ok && items < compute_units())) {
         const int64_t per_head = host_steps_before(*p, a.q_tiles - 1) +
                                  host_tile_steps(*p, a.q_tiles - 1);
         StreamArgs sa;
         sa.per_head = per_head;
         sa.units = per_head * p->batch * Hq;
         sa.counters = static_cast<uint32_t *>(workspace);
-        sa.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + stream_counter_bytes(*p));
+        sa.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + kStreamCounterBytes);
         if (sa.units >= (int64_t(1) << 40)) return REEF_UNSUPPORTED;
         // No more workgroups than steps: every range holds at least one step, so the
         // workgroups between an item's first and last part each hold a part of it.
-        const dim3 sgrid((unsigned)std::min<int64_t>(stream_groups(), sa.units));
-        if (D == 128)
-            hipLaunchKernelGGL(prefill_stream_kernel<128>, sgrid, dim3(kThreads), 0, stream, a, sa);
-        else
-            hipLaunchKernelGGL(prefill_stream_kernel<64>, sgrid, dim3(kThreads), 0, stream, a, sa);
+        // The precise kernels hold a compute unit alone: at most one workgroup per
+        // unit, so that every workgroup runs at once, and at least kStreamMinSteps
+        // steps per workgroup, so that a short chunk of queries over a long prefix is
+        // cut into a few parts per item (each merge reads its parts one after another).
+        const int64_t groups =
+            (tok || precise) ? std::max<int64_t>(1, std::min<int64_t>(compute_units(),
+                                                                      sa.units / kStreamMinSteps))
+                             : stream_groups();
+        const dim3 sgrid((unsigned)std::min<int64_t>(groups, sa.units));
+#define REEF_STREAM_LAUNCH(DIM, TOK, PREC)                                                   \
+    hipLaunchKernelGGL((prefill_stream_kernel<DIM, TOK, PREC>), sgrid, dim3(kThreads), 0, stream, \
+                       a, sa)
+        if (D == 128) {
+            if (tok) REEF_STREAM_LAUNCH(128, true, true);
+            else if (precise) REEF_STREAM_LAUNCH(128, false, true);
+            else REEF_STREAM_LAUNCH(128, false, false);
+        } else {
+            if (tok) REEF_STREAM_LAUNCH(64, true, true);
+            else if (precise) REEF_STREAM_LAUNCH(64, false, true);
+            else REEF_STREAM_LAUNCH(64, false, false);
+        }
+#undef REEF_STREAM_LAUNCH
         return launch_status();
     }
     const bool split = sched == REEF_ATTN_SCHED_SPLIT;

@@ -9,11 +9,16 @@
 // not read. One gather launch copies the kv_len cached tokens of every (sequence,
 // kv head) into token-major int8 rows and per-token scales in the workspace, page
 // by page (the values transposed back through LDS); the prefill entry point then
-// runs over them with per-token K/V scales. The gather moves 2 (D + 4) bytes per
+// runs over them with per-token K/V scales, on the balanced schedule when the
+// chunk has fewer 128-row query tiles than the GPU has compute units (its
+// workspace is the first part of this one). The gather moves 2 (D + 4) bytes per
 // cached token and kv head each way, small beside the chunk's attention.
 #include "reef_common.hpp"
 
 namespace reef {
+
+int64_t prefill_balanced_bytes(const reef_attention_params &p);  // prefill.hip
+
 namespace {
 
 constexpr int kPage = 16;
@@ -98,17 +103,20 @@ __global__ __launch_bounds__(kGatherThreads) void gather_cache(GatherArgs a) {
 
 int64_t round256(int64_t n) { return ceil_div(n, 256) * 256; }
 
-// Workspace layout: gathered keys, values (int8 rows), key scales, value scales.
+// Workspace layout: the prefill's balanced-schedule workspace (item counters, zero
+// between calls, and part slots), then the gathered keys and values (int8 rows),
+// key scales and value scales.
 struct CacheWorkspace {
-    int64_t k, v, ks, vs, total;
+    int64_t balanced, k, v, ks, vs, total;
 };
 
 CacheWorkspace cache_workspace(const reef_attention_params *p) {
     const int64_t rows = p->batch * p->kv_heads * p->kv_len;
     CacheWorkspace w;
-    w.k = 0;
-    w.v = round256(rows * p->head_dim);
-    w.ks = 2 * w.v;
+    w.balanced = round256(prefill_balanced_bytes(*p));
+    w.k = w.balanced;
+    w.v = w.k + round256(rows * p->head_dim);
+    w.ks = w.v + round256(rows * p->head_dim);
     w.vs = w.ks + round256(rows * 4);
     w.total = w.vs + round256(rows * 4);
     return w;
@@ -139,7 +147,8 @@ extern "C" reef_status reef_attention_prefill_int8_cache(
         p->query_start + p->q_len > p->kv_len || p->kv_granularity != REEF_SCALE_PER_TOKEN)
         return REEF_INVALID_ARGUMENT;
     if (p->head_dim != 64 && p->head_dim != 128) return REEF_UNSUPPORTED;
-    if (p->kv_len >= (int64_t(1) << 30) || p->batch * p->kv_heads > 65535)
+    if (p->kv_len >= (int64_t(1) << 30) || p->batch * p->kv_heads > 65535 ||
+        p->q_heads > 65535 || p->batch > 65535)
         return REEF_UNSUPPORTED;
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(k_scales, 4) ||
         !aligned(v_scales, 4))
@@ -181,6 +190,6 @@ extern "C" reef_status reef_attention_prefill_int8_cache(
         hipLaunchKernelGGL(gather_cache<64>, grid, dim3(kGatherThreads), 0, stream, g);
     if (launch_status() != REEF_OK) return REEF_HIP_ERROR;
     return reef_attention_prefill_int8(p, q, q_strides, g.k_out, nullptr, g.v_out, nullptr,
-                                       q_scales, g.ks_out, g.vs_out, out, out_strides, nullptr,
-                                       0, stream);
+                                       q_scales, g.ks_out, g.vs_out, out, out_strides, workspace,
+                                       (size_t)w.balanced, stream);
 }

@@ -75,16 +75,17 @@ def test_prefill_workspace_bytes_and_alignment():
     lib = reef_amd.lib()
     p = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048)
     n = lib.reef_attention_prefill_workspace_bytes(C.byref(p))
-    # item counters (512 items), then two partial slots per workgroup, two workgroups per
-    # compute unit (256 without a GPU): 128 x 128 outputs plus (max, sum) of 128 rows;
-    # then the packed value image: 32 tiles of 64 keys per head, 16 KB each, and one
-    # 4-byte block maximum per tile
-    balanced = 2048 + 2 * 512 * (128 * 128 + 2 * 256) * 4
+    # a fixed region of 65536 item counters, then two partial slots per workgroup, two
+    # workgroups per compute unit (256 without a GPU): 128 x 128 outputs plus (max,
+    # sum) of 128 rows; then the packed value image: 32 tiles of 64 keys per head,
+    # 16 KB each, and one 4-byte block maximum per tile
+    balanced = 65536 * 4 + 2 * 512 * (128 * 128 + 2 * 256) * 4
     image = 32 * 32 * 16384 + 32 * 32 * 4
     assert n == balanced + image
     p64 = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048, head_dim=64)
-    assert lib.reef_attention_prefill_workspace_bytes(C.byref(p64)) == \
-        2048 + 2 * 512 * (128 * 64 + 2 * 256) * 4  # no packed schedule at head_dim 64
+    # the same balanced region (slots sized for head_dim 128, so that every shape finds
+    # its counters at the same offsets); no packed schedule at head_dim 64
+    assert lib.reef_attention_prefill_workspace_bytes(C.byref(p64)) == balanced
     assert lib.reef_attention_prefill_workspace_bytes(C.byref(good_params(head_dim=96))) == 0
     assert lib.reef_attention_prefill_workspace_bytes(None) == 0
     # a workspace that is not 256-byte aligned
@@ -106,9 +107,12 @@ def test_prefill_cache_host_validation_and_workspace():
     lib = reef_amd.lib()
     tok = dict(kv_granularity=2, q_len=8, kv_len=40, query_start=32)
     p = good_params(**tok)
-    # 1 x 2 kv heads x 40 tokens: keys and values (80 rows x 128 bytes, rounded to
-    # 256), then two scale arrays (80 floats, rounded to 256)
-    assert lib.reef_attention_prefill_cache_workspace_bytes(C.byref(p)) == 2 * 10240 + 2 * 512
+    # the prefill's balanced-schedule workspace (a fixed region of 65536 counters; two
+    # part slots per workgroup, 2 x 256 workgroups without a GPU), then 1 x 2 kv heads x 40 tokens of keys and values (80 rows x 128 bytes,
+    # rounded to 256) and two scale arrays (80 floats, rounded to 256)
+    balanced = 65536 * 4 + 2 * 512 * (128 * 128 + 2 * 256) * 4
+    assert lib.reef_attention_prefill_cache_workspace_bytes(C.byref(p)) == \
+        balanced + 2 * 10240 + 2 * 512
     assert lib.reef_attention_prefill_cache_workspace_bytes(C.byref(good_params(head_dim=96))) == 0
     assert _prefill_cache(good_params(**dict(tok, kv_granularity=1))) == reef_amd.INVALID_ARGUMENT
     assert _prefill_cache(good_params(**dict(tok, query_start=33))) == reef_amd.INVALID_ARGUMENT
@@ -126,18 +130,19 @@ def test_decode_host_validation_and_workspace():
     p = DecodeParams(batch=64, q_heads=32, kv_heads=8, head_dim=128, max_context=4096,
                      window=0, softmax_scale=0.1, q_granularity=2, num_splits=0, flags=0)
     ws = lib.reef_attention_decode_workspace_bytes(C.byref(p))
-    # one counter per (sequence, kv head), then two part slots (64 lanes x 17
-    # eight-byte words) per workgroup: 2 workgroups per compute unit (256 without a
-    # GPU), the 512 items' 64-key blocks dealt out among them
+    # a fixed region of 2048 counters (one per (sequence, kv head) of a launch that
+    # deals out blocks), then two part slots (64 lanes x 17 eight-byte words) per
+    # workgroup of the larger (paged) launch: 2 workgroups per compute unit (256
+    # without a GPU), the 512 items' 64-key blocks dealt out among them
     slot = 17 * 64 * 8
-    assert ws == 2048 + 512 * 2 * slot
+    assert ws == 8192 + 512 * 2 * slot
     many = DecodeParams(64, 32, 8, 128, 4096, 0, 0.1, 2, 9, 0)
     # num_splits 9: 512 items x 9 / 4 waves = 1152 workgroups
-    assert lib.reef_attention_decode_workspace_bytes(C.byref(many)) == 2048 + 1152 * 2 * slot
+    assert lib.reef_attention_decode_workspace_bytes(C.byref(many)) == 8192 + 1152 * 2 * slot
     # more items than the in-workgroup plan holds (2048): whole items per workgroup,
-    # no part slots
+    # no part slots (and no counting)
     big = DecodeParams(4096, 8, 1, 128, 4096, 0, 0.1, 2, 0, 0)
-    assert lib.reef_attention_decode_workspace_bytes(C.byref(big)) == 4096 * 4
+    assert lib.reef_attention_decode_workspace_bytes(C.byref(big)) == 8192
     f = [_fake(i) for i in range(1, 12)]
     args = lambda pp, w: (C.byref(pp), f[0], f[1], f[2], f[3], f[4], f[5], None, f[6], f[7],  # noqa: E731
                           w, None, None)

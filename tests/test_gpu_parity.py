@@ -265,12 +265,13 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
                        softmax_scale=(1 / math.sqrt(D)) if scale is None else scale,
                        q_granularity=gq, kv_granularity=gkv)
     # both fp16 P and split P; the library's choice with and without a workspace, and
-    # every schedule forced through the flags (the split and balanced schedules do
-    # not take per-token K/V scales)
+    # every schedule forced through the flags (the split schedule takes neither
+    # per-token K/V scales nor the split P)
     runs = [(False, reef.SCHED_AUTO, None), (False, reef.SCHED_AUTO, False),
-            (False, reef.SCHED_ONE_ITEM, False), (True, reef.SCHED_AUTO, None)]
+            (False, reef.SCHED_ONE_ITEM, False), (True, reef.SCHED_AUTO, None),
+            (False, reef.SCHED_BALANCED, None), (True, reef.SCHED_BALANCED, None)]
     if gkv != 2:
-        runs += [(False, reef.SCHED_SPLIT, False), (False, reef.SCHED_BALANCED, None)]
+        runs += [(False, reef.SCHED_SPLIT, False)]
         if D == 128:
             runs += [(False, reef.SCHED_PACKED, None), (True, reef.SCHED_PACKED, None)]
     for precise, sched, ws in runs:
@@ -349,6 +350,10 @@ STREAM_CASES = [
     (2, 3, 1, 1000, 1500, 64, None, 300, 0),   # window, query_start 500, ragged last tile
     (1, 2, 2, 700, 900, 128, 150, 0, 1),       # explicit start below kv_len - q_len
     (3, 16, 4, 384, 384, 64, None, 0, 1),      # whole items between cut ones
+    # per-token K/V scales (hi + lo P): a 512-token chunk over a 4096-token prefix
+    # (the prefill over the cache), and a windowed GQA case
+    (1, 8, 1, 512, 4096, 128, None, 0, 2),
+    (2, 4, 2, 300, 1000, 64, None, 128, 2),
 ]
 
 
@@ -375,7 +380,8 @@ def test_prefill_balanced_schedule(reef, B, Hq, Hkv, Sq, Skv, D, start, window, 
     ws = torch.zeros(n, dtype=torch.uint8, device="cuda")
     args = (gpu(qq), gpu(kq), gpu(vq), gpu(qs), gpu(ks), gpu(vs))
     kw = dict(query_start=p.start(), window=window, softmax_scale=p.softmax_scale,
-              q_granularity=gran, kv_granularity=gran, workspace=ws)
+              q_granularity=gran, kv_granularity=gran, workspace=ws,
+              schedule=reef.SCHED_BALANCED)
     out1 = host(reef.attention_prefill(*args, **kw))
     out2 = host(reef.attention_prefill(*args, **kw))
     err = np.abs(out1 - gold).max()
@@ -592,3 +598,39 @@ def test_decode_paged_flags_bad_pages_and_lengths(reef):
     with pytest.raises(reef.InvalidArgument):
         reef.attention_decode_paged(gpu(qq), gpu(qs), gpu(kp), gpu(vp), gpu(ksp), gpu(vsp),
                                     gpu(table), gpu(np.array([40, 0], np.int32)))
+
+
+def test_workspaces_serve_calls_of_any_shape(reef):
+    """One zero-filled workspace reused by calls of different shapes: the balanced
+    prefill with 48 items and then 96 (a layout with a per-call number of counters
+    made the second call read the first call's part slots as counters), and decode
+    with 8 items and then 80. The counters sit at fixed offsets, so every call
+    matches the oracle."""
+    big = reef.AttentionParams(2, 16, 4, 300, 1000, 64, 700, 0, 0.125, 1, 1, 0)
+    ws = torch.zeros(reef.lib().reef_attention_prefill_workspace_bytes(reef.C.byref(big)),
+                     dtype=torch.uint8, device="cuda")
+    for B in (1, 2, 1, 2):
+        case(f"prefill balanced B{B} Hq16 Hkv4 Sq300 Skv1000 D64, one workspace")
+        seed = 400 + B
+        q = W.lcg_normal(seed, B * 16 * 300 * 64).reshape(B, 16, 300, 64)
+        k = W.lcg_normal(seed + 1, B * 4 * 1000 * 64).reshape(B, 4, 1000, 64)
+        v = W.lcg_normal(seed + 2, B * 4 * 1000 * 64).reshape(B, 4, 1000, 64)
+        p = oracle.Problem(B, 16, 4, 300, 1000, 64, softmax_scale=0.125)
+        out, gold = _run_prefill(reef, q, k, v, p, workspace=ws, schedule=reef.SCHED_BALANCED)
+        err = np.abs(out - gold).max()
+        print(f"max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL
+    D, Hq, Hkv = 128, 8, 2
+    dbig = reef.DecodeParams(40, Hq, Hkv, D, 640, 0, 1 / math.sqrt(D), reef.PER_TOKEN, 0, 0)
+    dws = reef.decode_workspace(dbig, "cuda")
+    for B in (4, 40, 4, 40):
+        lens = [int(x) for x in (np.arange(B) * 97 % 630 + 1)]
+        case(f"decode B{B} Hq{Hq} Hkv{Hkv}, one workspace")
+        qq, qs, kq, ks, vq, vs = _decode_problem(B, Hq, Hkv, D, lens, 500 + B, 640)
+        out = reef.attention_decode(gpu(qq), gpu(qs), gpu(kq), reef.pack_v_pages(gpu(vq)),
+                                    gpu(ks), gpu(vs), gpu(np.array(lens, np.int32)),
+                                    softmax_scale=1 / math.sqrt(D), workspace=dws)
+        gold = _decode_gold(qq, qs, kq, ks, vq, vs, lens, 0, 1 / math.sqrt(D))
+        err = np.abs(host(out) - gold).max()
+        print(f"max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL
