@@ -449,6 +449,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
                 }
                 rs_hi = mfma_16x16x32_f16(ones, operand(phi), rs_hi);
                 if (LO) rs_lo = mfma_16x16x32_f16(ones, operand(plo), rs_lo);
+                __builtin_amdgcn_s_setprio(1);
 #pragma unroll
                 for (int d = 0; d < DB; ++d) acc[d] = mfma_32x32x16_f16(vop[d], operand(phi), acc[d]);
                 if (LO) {
@@ -457,6 +458,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
                         if ((pmask >> d) & 1)  // uniform
                             acc[d] = mfma_32x32x16_f16(vop[d], operand(plo), acc[d]);
                 }
+                __builtin_amdgcn_s_setprio(0);
             }
     };
 
@@ -504,7 +506,14 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         __builtin_amdgcn_s_barrier();
         issue_group(j + 2);
         Scores next;
-        tile_math(j, masked_tag, cur, [&] { next = scores(j + 1); });
+        // The wave raises its issue priority while it issues matrix instructions, so
+        // that of the two waves on a SIMD the one with products to issue goes first
+        // and the other fills in with its vector work (2.4 % on 4x32x8192x128).
+        tile_math(j, masked_tag, cur, [&] {
+            __builtin_amdgcn_s_setprio(1);
+            next = scores(j + 1);
+            __builtin_amdgcn_s_setprio(0);
+        });
         return next;
     };
     // Two tiles per iteration: the loop-carried scores come back in the registers
