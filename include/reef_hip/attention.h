@@ -146,16 +146,18 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
 /* Prefill work schedule (bits 4-6 of flags). AUTO lets the library choose from the
  * grid size and the workspace; the others force one schedule, for callers that
  * tune it and for tests that must reach every path. A forced schedule that the
- * call cannot use (BALANCED without a large enough workspace, SPLIT with PRECISE_PV
- * or PER_TOKEN K/V scales, PACKED without head_dim 128, per-tensor or per-head K/V
- * scales and a workspace) returns REEF_INVALID_ARGUMENT. AUTO takes BALANCED for a
- * call with PRECISE_PV or PER_TOKEN K/V scales, a large enough workspace and fewer
- * 128-row query tiles than compute units. */
+ * call cannot use (BALANCED without a large enough workspace, SPLIT with PER_TOKEN
+ * K/V scales, PACKED without head_dim 128, per-tensor or per-head K/V scales and a
+ * workspace) returns REEF_INVALID_ARGUMENT. AUTO takes BALANCED for a call with
+ * PRECISE_PV or PER_TOKEN K/V scales, a large enough workspace and fewer 128-row
+ * query tiles than compute units, and SPLIT for other calls with at most one such
+ * tile per compute unit. */
 #define REEF_ATTN_SCHED_MASK 0x70u
 #define REEF_ATTN_SCHED_AUTO 0x00u
 #define REEF_ATTN_SCHED_ONE_ITEM 0x10u /* one 128-row query tile per workgroup */
 #define REEF_ATTN_SCHED_SPLIT 0x20u    /* persistent workgroups; two 4-wave groups split
-                                        * each tile's keys */
+                                        * each tile's keys; hi + lo P where the values
+                                        * need it or with PRECISE_PV */
 #define REEF_ATTN_SCHED_BALANCED 0x30u /* equal (tile, key block) ranges per workgroup;
                                         * cut tiles merge through the workspace; hi + lo
                                         * P with PRECISE_PV or PER_TOKEN K/V scales */

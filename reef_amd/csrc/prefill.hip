@@ -726,12 +726,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     }
 }
 
+// Whether the values of (batch b, query head h)'s kv head reach above kPreciseAbove
+// (per-tensor or per-head value scales): such items take P split into hi + lo.
+__device__ __forceinline__ bool item_is_wide(const PrefillArgs &a, int b, int h) {
+    const int kvh = h / (a.q_heads / a.kv_heads);
+    return 127.0f * scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) > kPreciseAbove;
+}
+
 // Persistent form of the split kernel: one workgroup per compute unit takes the
 // items of round r = 0, 1, ... at index r * G + blockIdx.x, the odd rounds in
 // reverse order, so that with heaviest-first ranks every workgroup's sum of work
 // is about the same. A workgroup's next item starts while the stores of its last
 // one drain.
-template <int D>
+template <int D, bool PRECISE>
 __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillArgs a, int items) {
     static_assert(4 * (D / 32) * 4 * kWave * 16 + 4 * kWave * 8 <= 2 * PrefillLds<D>::BYTES,
                   "merge buffer fits in the stages");
@@ -746,8 +753,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillA
         }
         int tile, b, h;
         item_coords(a, item, tile, b, h);
-        prefill_body<D, false, false, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
-                                              StreamPart{}, nullptr);
+        if (a.item_sel != 0 && item_is_wide(a, b, h) != (a.item_sel == 2)) continue;  // uniform
+        prefill_body<D, false, PRECISE, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
+                                                StreamPart{}, nullptr);
         __syncthreads();  // the next item's stages overwrite the merge buffer
     }
 }
@@ -758,12 +766,7 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
     int tile, b, h;
     item_coords(a, grid_rank(a), tile, b, h);
-    if (!KV_TOKEN && a.item_sel != 0) {
-        const int kvh = h / (a.q_heads / a.kv_heads);
-        const bool wide = 127.0f * scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) >
-                          kPreciseAbove;
-        if (wide != (a.item_sel == 2)) return;
-    }
+    if (!KV_TOKEN && a.item_sel != 0 && item_is_wide(a, b, h) != (a.item_sel == 2)) return;
     prefill_body<D, KV_TOKEN, PRECISE, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
                                                StreamArgs{}, StreamPart{}, nullptr);
 }
@@ -1040,15 +1043,18 @@ extern "C" reef_status reef_attention_prefill_int8(
         return prefill_packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out,
                                      ost, static_cast<char *>(workspace) + bal_bytes, stream);
     }
-    // The split schedule rounds P to one fp16 (11 bits); the balanced one takes P
-    // split into hi + lo when the call asks for precision (per-token K/V scales
-    // always do). Without a request for precision the library leaves both to callers
-    // that force them, and the one-item kernel splits P where the values need it (per
-    // item, two launches). With precision and fewer 128-row tiles than compute units
-    // (a short chunk of queries over a long cache), the library takes the balanced
-    // schedule: the one-item kernel would leave most of the GPU idle.
+    // The balanced schedule takes P split into hi + lo when the call asks for
+    // precision (per-token K/V scales always do); without a request for precision the
+    // library leaves it to callers that force it. With precision and fewer 128-row
+    // tiles than compute units (a short chunk of queries over a long cache), the
+    // library takes it: the one-item kernel would leave most of the GPU idle. The
+    // split and one-item kernels split P where the values need it (per item, two
+    // launches); with at most one item per compute unit the library takes the split
+    // kernel, whose key split is the only parallelism left to balance the causal work
+    // (1x8q/1kv x4096x128: 67 against 82 us); with more, two one-item workgroups per
+    // compute unit overlap each other's prologue and epilogue better.
     if (sched == REEF_ATTN_SCHED_BALANCED && !stream_ok) return REEF_INVALID_ARGUMENT;
-    if (sched == REEF_ATTN_SCHED_SPLIT && (tok || precise)) return REEF_INVALID_ARGUMENT;
+    if (sched == REEF_ATTN_SCHED_SPLIT && tok) return REEF_INVALID_ARGUMENT;
     a.item_sel = 0;
     if (sched == REEF_ATTN_SCHED_BALANCED ||
         (sched == REEF_ATTN_SCHED_AUTO && precise && stream_ok && items < compute_units())) {
@@ -1086,19 +1092,32 @@ extern "C" reef_status reef_attention_prefill_int8(
 #undef REEF_STREAM_LAUNCH
         return launch_status();
     }
-    const bool split = sched == REEF_ATTN_SCHED_SPLIT;
+    const bool split = sched == REEF_ATTN_SCHED_SPLIT ||
+                       (sched == REEF_ATTN_SCHED_AUTO && !tok && items <= compute_units());
     // The 4-wave kernel places two workgroups on each of the 256 compute units at
     // once; zig-zag pairs a heavy and a light tile there. The split kernel holds a
     // compute unit alone and takes the tiles heaviest first.
     a.zigzag = !split && items <= 2 * compute_units() ? 1 : 0;
     if (split) {
         const dim3 pgrid((unsigned)std::min<int64_t>(items, compute_units()));
-        if (D == 128)
-            hipLaunchKernelGGL(prefill_split_kernel<128>, pgrid, dim3(2 * kThreads), 0, stream, a,
-                               (int)items);
-        else
-            hipLaunchKernelGGL(prefill_split_kernel<64>, pgrid, dim3(2 * kThreads), 0, stream, a,
-                               (int)items);
+#define REEF_SPLIT_LAUNCH(DIM, PREC)                                                         \
+    hipLaunchKernelGGL((prefill_split_kernel<DIM, PREC>), pgrid, dim3(2 * kThreads), 0, stream, a, \
+                       (int)items)
+        if (precise) {
+            if (D == 128) REEF_SPLIT_LAUNCH(128, true);
+            else REEF_SPLIT_LAUNCH(64, true);
+            return launch_status();
+        }
+        // Items whose values stay within kPreciseAbove take one fp16 P, the others the
+        // hi + lo split; each launch skips the other's items.
+        a.item_sel = 1;
+        if (D == 128) REEF_SPLIT_LAUNCH(128, false);
+        else REEF_SPLIT_LAUNCH(64, false);
+        if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
+        a.item_sel = 2;
+        if (D == 128) REEF_SPLIT_LAUNCH(128, true);
+        else REEF_SPLIT_LAUNCH(64, true);
+#undef REEF_SPLIT_LAUNCH
         return launch_status();
     }
 #define REEF_PREFILL_LAUNCH(DIM, TOK, PREC)                                                  \

@@ -265,13 +265,13 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
                        softmax_scale=(1 / math.sqrt(D)) if scale is None else scale,
                        q_granularity=gq, kv_granularity=gkv)
     # both fp16 P and split P; the library's choice with and without a workspace, and
-    # every schedule forced through the flags (the split schedule takes neither
-    # per-token K/V scales nor the split P)
+    # every schedule forced through the flags (the split schedule takes no per-token
+    # K/V scales)
     runs = [(False, reef.SCHED_AUTO, None), (False, reef.SCHED_AUTO, False),
             (False, reef.SCHED_ONE_ITEM, False), (True, reef.SCHED_AUTO, None),
             (False, reef.SCHED_BALANCED, None), (True, reef.SCHED_BALANCED, None)]
     if gkv != 2:
-        runs += [(False, reef.SCHED_SPLIT, False)]
+        runs += [(False, reef.SCHED_SPLIT, False), (True, reef.SCHED_SPLIT, False)]
         if D == 128:
             runs += [(False, reef.SCHED_PACKED, None), (True, reef.SCHED_PACKED, None)]
     for precise, sched, ws in runs:
@@ -286,7 +286,8 @@ def test_prefill_outlier_channels(reef):
     """Per-head scales with a few value channels scaled x8 (activation outliers):
     the values of those heads reach |v| ~ 30, where one fp16 P is not precise enough.
     Every schedule the library chooses by itself (packed with a workspace, the
-    one-item kernel without) and the forced precise split stay within TOL."""
+    one-item kernel without), the forced precise one-item kernel and the forced split
+    kernel (hi + lo P on the outlier heads) stay within TOL."""
     B, H, S, D = 1, 4, 1100, 128
     case(f"prefill outlier channels B{B} H{H} S{S} D{D}")
     q = W.lcg_normal(801, B * H * S * D).reshape(B, H, S, D)
@@ -298,7 +299,7 @@ def test_prefill_outlier_channels(reef):
     p = oracle.Problem(B, H, H, S, S, D, softmax_scale=1 / math.sqrt(D))
     runs = [(False, reef.SCHED_AUTO, None), (False, reef.SCHED_AUTO, False),
             (False, reef.SCHED_PACKED, None), (False, reef.SCHED_ONE_ITEM, False),
-            (True, reef.SCHED_ONE_ITEM, False)]
+            (True, reef.SCHED_ONE_ITEM, False), (False, reef.SCHED_SPLIT, False)]
     for precise, sched, ws in runs:
         out, gold = _run_prefill(reef, q, k, v, p, precise, workspace=ws, schedule=sched)
         err = np.abs(out - gold).max()
