@@ -69,6 +69,20 @@ int main() {
                                             f32, nullptr, nullptr, nullptr),
                         "kv append");
     }, "KV cache capacity exceeded");
+    // the prefill over the cache: the cache's per-token scales are required, and a
+    // contiguous cache shorter than kv_len is refused
+    reef_attention_params chunk = p;
+    chunk.kv_len = 40;
+    chunk.query_start = 32;
+    expect<std::invalid_argument>("context_cache without per-token K/V scales", [&] {
+        reef_hip::context_cache(chunk, i8, nullptr, f32, i8, i8, f32, f32, 64, nullptr, 0, 0, f32,
+                                nullptr, i8, 1 << 30, nullptr, nullptr);
+    });
+    chunk.kv_granularity = REEF_SCALE_PER_TOKEN;
+    expect<std::invalid_argument>("context_cache on a cache shorter than kv_len", [&] {
+        reef_hip::context_cache(chunk, i8, nullptr, f32, i8, i8, f32, f32, 32, nullptr, 0, 0, f32,
+                                nullptr, i8, 1 << 30, nullptr, nullptr);
+    });
     expect<reef_hip::hip_error>("hip error status", [&] { reef_hip::check(REEF_HIP_ERROR, "x"); });
     std::printf("%d failures\n", failures);
     return failures == 0 ? 0 : 1;
