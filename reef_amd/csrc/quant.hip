@@ -7,14 +7,35 @@
 //
 // Every kernel here is bound by HBM bandwidth: 4 bytes read and 1 byte written
 // per element (per-tensor and per-head scales need the whole tensor's maximum
-// first, so those read the input twice; the second read usually hits the
-// 256 MB last-level cache).
+// first, so those read the input twice). Streams larger than the last-level cache
+// use non-temporal accesses: nothing of them is found in a cache again, and
+// without the allocation they run a quarter to a third faster (a per-head
+// quantize of 4 x 32 x 8192 x 128 floats, 537 MB: 214 against 277 us; a
+// dequantize to 537 MB of floats: 97 against 157 us). Smaller ones use ordinary
+// accesses, and the second read of a two-pass scale finds much of the first in
+// the 256 MB last-level cache.
 #include "reef_common.hpp"
 
 namespace reef {
 namespace {
 
 constexpr int kQuantThreads = 256;
+// Inputs (or outputs) beyond these sizes are streamed with non-temporal accesses:
+// one-pass kernels beyond the 256 MB last-level cache, the two-pass per-tensor and
+// per-head scales beyond 384 MB (at 268 MB the second read still finds enough of
+// the first in the cache: 97 against 108 us with non-temporal loads).
+constexpr int64_t kStreamBytes = int64_t(256) << 20;
+constexpr int64_t kStreamBytesTwoPass = int64_t(384) << 20;
+
+template <bool NT>
+__device__ __forceinline__ float4 load4(const float4 *p) {
+    if constexpr (NT) {
+        const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+        return float4{t[0], t[1], t[2], t[3]};
+    } else {
+        return *p;
+    }
+}
 
 // Largest magnitudes are reduced as the bit patterns of |x|: for non-negative
 // floats the unsigned order of the bits is the float order, and any Inf or NaN
@@ -208,7 +229,8 @@ struct FlatHeads {
     int32_t heads, batch, blocks;  // blocks per slice
 };
 
-constexpr int kFlatUnroll = 8;
+constexpr int kFlatUnroll = 4;
+constexpr int64_t kFlatBlocks = 2048;  // about 8 per compute unit: 128 KB of loads in flight per unit
 
 __device__ __forceinline__ uint32_t block_max(uint32_t m) {  // the result on thread 0
     __shared__ uint32_t partial[kQuantThreads / kWave];
@@ -226,7 +248,7 @@ __device__ __forceinline__ int64_t chunk_word(const FlatHeads &f, int b, int h, 
     return ((int64_t)b * f.heads + h) * f.slice4 + (int64_t)x * f.chunk4;
 }
 
-template <bool kSpread>
+template <bool kSpread, bool NT>
 __global__ __launch_bounds__(kQuantThreads) void head_max_flat(FlatHeads f, uint32_t *partials) {
     const int h = blockIdx.y, b = blockIdx.z;
     const float4 *x = reinterpret_cast<const float4 *>(f.x + b * f.sb + h * f.sh);
@@ -238,7 +260,7 @@ __global__ __launch_bounds__(kQuantThreads) void head_max_flat(FlatHeads f, uint
 #pragma unroll
         for (int u = 0; u < kFlatUnroll; ++u) {
             const int64_t j = i + u * kQuantThreads;
-            v[u] = j < i1 ? x[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            v[u] = j < i1 ? load4<NT>(x + j) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
         for (int u = 0; u < kFlatUnroll; ++u) {
@@ -278,7 +300,7 @@ __global__ __launch_bounds__(kQuantThreads) void head_scale_flat(FlatHeads f,
 
 // kSpread: the scale comes from the partial words in this block's own chunk of q
 // (written by the max pass), and block (0, h, 0) stores it to scales[h].
-template <bool kSpread>
+template <bool kSpread, bool NT>
 __global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f, float *scales,
                                                                     int8_t *__restrict__ q,
                                                                     uint32_t *status) {
@@ -309,7 +331,7 @@ __global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f,
 #pragma unroll
         for (int u = 0; u < kFlatUnroll; ++u) {
             const int64_t j = i + u * kQuantThreads;
-            v[u] = j < i1 ? x[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            v[u] = j < i1 ? load4<NT>(x + j) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
         for (int u = 0; u < kFlatUnroll; ++u) {
@@ -332,60 +354,79 @@ __global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f,
 //
 // Fast form for rows of at most 256 float4 (width % 4 == 0): LPR lanes per row hold
 // the row's float4 in registers (PER each), so the row is read once; 64 / LPR rows
-// per wave. The largest magnitude is reduced over the LPR lanes of the row.
+// per wave and row group. The largest magnitude is reduced over the LPR lanes of the
+// row. Streams beyond the cache take row_groups groups per wave whose loads are all
+// issued before the first group is reduced (4 float4 in flight per lane: 1M rows of
+// 128 in 126 against 149 us); smaller inputs one group per wave (more, shorter
+// waves: 65536 rows of 128 in 10.9 against 12.8 us).
+__host__ __device__ constexpr int row_groups(int per, bool nt) {
+    return nt && per < 4 ? 4 / per : 1;
+}
 
-template <int LPR, int PER>
+template <int LPR, int PER, bool NT>
 __global__ __launch_bounds__(kQuantThreads) void token_quantize_regs(
     const float *__restrict__ x, int64_t rows, int32_t w4, int64_t row_stride,
     int8_t *__restrict__ q, float *__restrict__ scales, uint32_t *status) {
-    constexpr int RPW = kWave / LPR;  // rows per wave
+    constexpr int RPW = kWave / LPR;  // rows per wave and group
+    constexpr int G = row_groups(PER, NT);
     const int lane = threadIdx.x % kWave, sub = lane / LPR, l = lane % LPR;
-    const int64_t row =
-        ((int64_t)blockIdx.x * (kQuantThreads / kWave) + threadIdx.x / kWave) * RPW + sub;
-    const bool live = row < rows;
-    const float4 *r = reinterpret_cast<const float4 *>(x + (live ? row : 0) * row_stride);
-    float4 v[PER];
-    uint32_t m = 0;
+    const int64_t wave_id = (int64_t)blockIdx.x * (kQuantThreads / kWave) + threadIdx.x / kWave;
+    float4 v[G][PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int col = l + j * LPR;
-        v[j] = (live && col < w4) ? r[col] : float4{0.0f, 0.0f, 0.0f, 0.0f};
-        uint32_t a = mag_bits(v[j].x), b = mag_bits(v[j].y), c = mag_bits(v[j].z),
-                 d = mag_bits(v[j].w);
-        a = a > b ? a : b;
-        c = c > d ? c : d;
-        a = a > c ? a : c;
-        m = m > a ? m : a;
-    }
+    for (int g = 0; g < G; ++g) {
+        const int64_t row = (wave_id * G + g) * RPW + sub;
+        const bool live = row < rows;
+        const float4 *r = reinterpret_cast<const float4 *>(x + (live ? row : 0) * row_stride);
 #pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) {
-        const uint32_t w = (uint32_t)__shfl_xor((int)m, o);
-        m = m > w ? m : w;
-    }
-    const float scale = int8_scale(__uint_as_float(m));
-    if (!live) return;
-    char4 *out = reinterpret_cast<char4 *>(q + row * (int64_t)w4 * 4);
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int col = l + j * LPR;
-        if (col < w4) {
-            char4 c;
-            c.x = quantize_int8(v[j].x, scale);
-            c.y = quantize_int8(v[j].y, scale);
-            c.z = quantize_int8(v[j].z, scale);
-            c.w = quantize_int8(v[j].w, scale);
-            out[col] = c;
+        for (int j = 0; j < PER; ++j) {
+            const int col = l + j * LPR;
+            v[g][j] = (live && col < w4) ? load4<NT>(r + col) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
-    if (l == 0) {
-        scales[row] = scale;
-        if (m >= 0x7f800000u) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int64_t row = (wave_id * G + g) * RPW + sub;
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            uint32_t a = mag_bits(v[g][j].x), b = mag_bits(v[g][j].y), c = mag_bits(v[g][j].z),
+                     d = mag_bits(v[g][j].w);
+            a = a > b ? a : b;
+            c = c > d ? c : d;
+            a = a > c ? a : c;
+            m = m > a ? m : a;
+        }
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) {
+            const uint32_t w = (uint32_t)__shfl_xor((int)m, o);
+            m = m > w ? m : w;
+        }
+        const float scale = int8_scale(__uint_as_float(m));
+        if (row < rows) {
+            char4 *out = reinterpret_cast<char4 *>(q + row * (int64_t)w4 * 4);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int col = l + j * LPR;
+                if (col < w4) {
+                    char4 c;
+                    c.x = quantize_int8(v[g][j].x, scale);
+                    c.y = quantize_int8(v[g][j].y, scale);
+                    c.z = quantize_int8(v[g][j].z, scale);
+                    c.w = quantize_int8(v[g][j].w, scale);
+                    out[col] = c;
+                }
+            }
+            if (l == 0) {
+                scales[row] = scale;
+                if (m >= 0x7f800000u) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
+            }
+        }
     }
 }
 
 // Wide rows (256 < width / 4 <= 256 * PER): one block per row, PER float4 per
 // thread held in registers, the largest magnitude reduced across the block.
-template <int PER>
+template <int PER, bool NT>
 __global__ __launch_bounds__(kQuantThreads) void token_quantize_wide(
     const float *__restrict__ x, int32_t w4, int64_t row_stride, int8_t *__restrict__ q,
     float *__restrict__ scales, uint32_t *status) {
@@ -397,7 +438,7 @@ __global__ __launch_bounds__(kQuantThreads) void token_quantize_wide(
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int col = threadIdx.x + j * kQuantThreads;
-        v[j] = col < w4 ? r[col] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[j] = col < w4 ? load4<NT>(r + col) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         uint32_t a = mag_bits(v[j].x), b = mag_bits(v[j].y), c = mag_bits(v[j].z),
                  d = mag_bits(v[j].w);
         a = a > b ? a : b;
@@ -458,7 +499,7 @@ __global__ __launch_bounds__(kQuantThreads) void token_quantize(const float *__r
 
 // x[i] = float(q[i]) * scales[i / group]. VEC: 4 values per thread (group % 4 == 0,
 // n a whole number of groups); `tpr` threads per group, 256 / tpr groups per step.
-template <bool VEC>
+template <bool VEC, bool NT>
 __global__ __launch_bounds__(kQuantThreads) void dequantize(const int8_t *__restrict__ q, int64_t n,
                                                             int64_t group, int32_t tpr,
                                                             const float *__restrict__ scales,
@@ -475,7 +516,11 @@ __global__ __launch_bounds__(kQuantThreads) void dequantize(const int8_t *__rest
             float4 *dst = reinterpret_cast<float4 *>(x + g * group);
             for (int64_t c = lane_c; c < per; c += tpr) {
                 const char4 v = src[c];
-                dst[c] = float4{(float)v.x * s, (float)v.y * s, (float)v.z * s, (float)v.w * s};
+                const f32x4 o = {(float)v.x * s, (float)v.y * s, (float)v.z * s, (float)v.w * s};
+                if constexpr (NT)
+                    __builtin_nontemporal_store(o, reinterpret_cast<f32x4 *>(dst + c));
+                else
+                    *reinterpret_cast<f32x4 *>(dst + c) = o;
             }
         } else {
             const int64_t e1 = min(n, (g + 1) * group);
@@ -487,22 +532,76 @@ __global__ __launch_bounds__(kQuantThreads) void dequantize(const int8_t *__rest
 // The flat kernels over f (q 4-byte aligned, at least 4 * batch * heads * blocks
 // bytes): two launches when the shortest chunk of q holds a head's batch * blocks
 // partial words, three otherwise.
-void launch_flat(const FlatHeads &f, int8_t *q, float *scales, uint32_t *status,
-                 hipStream_t stream) {
+template <bool NT>
+void launch_flat_nt(const FlatHeads &f, int8_t *q, float *scales, uint32_t *status,
+                    hipStream_t stream) {
     uint32_t *partials = reinterpret_cast<uint32_t *>(q);
     const dim3 grid((unsigned)f.blocks, (unsigned)f.heads, (unsigned)f.batch);
     const int64_t last4 = f.slice4 - (int64_t)(f.blocks - 1) * f.chunk4;  // shortest chunk
     if ((int64_t)f.batch * f.blocks <= std::min<int64_t>(last4, 512)) {
-        hipLaunchKernelGGL(head_max_flat<true>, grid, dim3(kQuantThreads), 0, stream, f, partials);
-        hipLaunchKernelGGL(head_quantize_flat<true>, grid, dim3(kQuantThreads), 0, stream, f,
+        hipLaunchKernelGGL((head_max_flat<true, NT>), grid, dim3(kQuantThreads), 0, stream, f,
+                           partials);
+        hipLaunchKernelGGL((head_quantize_flat<true, NT>), grid, dim3(kQuantThreads), 0, stream, f,
                            scales, q, status);
         return;
     }
-    hipLaunchKernelGGL(head_max_flat<false>, grid, dim3(kQuantThreads), 0, stream, f, partials);
+    hipLaunchKernelGGL((head_max_flat<false, NT>), grid, dim3(kQuantThreads), 0, stream, f,
+                       partials);
     hipLaunchKernelGGL(head_scale_flat, dim3((unsigned)f.heads), dim3(kQuantThreads), 0, stream,
                        f, (const uint32_t *)partials, scales);
-    hipLaunchKernelGGL(head_quantize_flat<false>, grid, dim3(kQuantThreads), 0, stream, f,
+    hipLaunchKernelGGL((head_quantize_flat<false, NT>), grid, dim3(kQuantThreads), 0, stream, f,
                        scales, q, status);
+}
+
+void launch_flat(const FlatHeads &f, int8_t *q, float *scales, uint32_t *status,
+                 hipStream_t stream) {
+    if (16 * f.slice4 * f.batch * f.heads > kStreamBytesTwoPass)
+        launch_flat_nt<true>(f, q, scales, status, stream);
+    else
+        launch_flat_nt<false>(f, q, scales, status, stream);
+}
+
+// The register and wide forms (width % 4 == 0, w4 = width / 4 <= 8 * kQuantThreads).
+template <bool NT>
+void launch_rows(const float *x, int64_t rows, int64_t w4, int64_t row_stride, int8_t *q,
+                 float *scales, uint32_t *status_word, hipStream_t stream) {
+    if (w4 <= 4 * kWave) {
+        // lanes per row: the smallest power of two >= w4 (up to 64), then up to 4
+        // float4 per lane
+        int lpr = 1;
+        while (lpr < w4 && lpr < kWave) lpr *= 2;
+        const int per = w4 <= kWave ? 1 : w4 <= 2 * kWave ? 2 : 4;  // float4 per lane
+        const int64_t rows_per_block =
+            (int64_t)(kWave / lpr) * row_groups(per, NT) * (kQuantThreads / kWave);
+        const dim3 grid((unsigned)ceil_div(rows, rows_per_block));
+#define REEF_TOKEN_LAUNCH(L, P)                                                               \
+    hipLaunchKernelGGL((token_quantize_regs<L, P, NT>), grid, dim3(kQuantThreads), 0, stream, \
+                       x, rows, (int32_t)w4, row_stride, q, scales, status_word)
+        switch (lpr) {
+        case 1: REEF_TOKEN_LAUNCH(1, 1); break;
+        case 2: REEF_TOKEN_LAUNCH(2, 1); break;
+        case 4: REEF_TOKEN_LAUNCH(4, 1); break;
+        case 8: REEF_TOKEN_LAUNCH(8, 1); break;
+        case 16: REEF_TOKEN_LAUNCH(16, 1); break;
+        case 32: REEF_TOKEN_LAUNCH(32, 1); break;
+        default:
+            if (per == 1) REEF_TOKEN_LAUNCH(64, 1);
+            else if (per == 2) REEF_TOKEN_LAUNCH(64, 2);
+            else REEF_TOKEN_LAUNCH(64, 4);
+        }
+#undef REEF_TOKEN_LAUNCH
+    } else {
+        const dim3 grid((unsigned)rows);
+        if (w4 <= 2 * kQuantThreads)
+            hipLaunchKernelGGL((token_quantize_wide<2, NT>), grid, dim3(kQuantThreads), 0,
+                               stream, x, (int32_t)w4, row_stride, q, scales, status_word);
+        else if (w4 <= 4 * kQuantThreads)
+            hipLaunchKernelGGL((token_quantize_wide<4, NT>), grid, dim3(kQuantThreads), 0,
+                               stream, x, (int32_t)w4, row_stride, q, scales, status_word);
+        else
+            hipLaunchKernelGGL((token_quantize_wide<8, NT>), grid, dim3(kQuantThreads), 0,
+                               stream, x, (int32_t)w4, row_stride, q, scales, status_word);
+    }
 }
 
 }  // namespace
@@ -522,8 +621,8 @@ extern "C" reef_status reef_quantize_int8_per_tensor(const float *x, int64_t n, 
         f.sb = f.sh = 0;
         f.slice4 = n / 4;
         f.heads = f.batch = 1;
-        const int64_t per_slice =
-            std::max<int64_t>(1, std::min<int64_t>(512, ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
+        const int64_t per_slice = std::max<int64_t>(
+            1, std::min<int64_t>(kFlatBlocks, ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
         f.chunk4 = ceil_div(f.slice4, per_slice);
         f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
         if (4 * (int64_t)f.blocks <= n) {
@@ -566,9 +665,9 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
     v.tpr = 1;
     while (v.tpr < v.per_row && v.tpr < kQuantThreads) v.tpr *= 2;
     if (vec && v.st == head_dim && batch <= 65535) {
-        // Contiguous tokens: flat float4 streams, about 512 blocks in all (2 per
-        // compute unit), at least 32 KB of input each; the partial maxima (4 bytes
-        // per block) fit in q when q holds at least that many bytes.
+        // Contiguous tokens: flat float4 streams, about kFlatBlocks blocks in all,
+        // at least 16 KB of input each; the partial maxima (4 bytes per block) fit
+        // in q when q holds at least that many bytes.
         FlatHeads f;
         f.x = x;
         f.sb = v.sb;
@@ -576,8 +675,9 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
         f.slice4 = tokens * head_dim / 4;
         f.heads = (int32_t)heads;
         f.batch = (int32_t)batch;
-        const int64_t per_slice = std::max<int64_t>(
-            1, std::min(ceil_div(512, batch * heads), ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
+        const int64_t per_slice =
+            std::max<int64_t>(1, std::min(ceil_div(kFlatBlocks, batch * heads),
+                                          ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
         f.chunk4 = ceil_div(f.slice4, per_slice);
         f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
         const int64_t partial_bytes = 4 * batch * heads * (int64_t)f.blocks;
@@ -618,40 +718,11 @@ extern "C" reef_status reef_quantize_int8_per_token(const float *x, int64_t rows
         return REEF_INVALID_ARGUMENT;
     const bool vec = width % 4 == 0 && row_stride % 4 == 0 && aligned(x, 16) && aligned(q, 4);
     const int64_t w4 = width / 4;
-    if (vec && w4 <= 4 * kWave) {
-        // lanes per row: the smallest power of two >= w4 (up to 64), then up to 4
-        // float4 per lane
-        int lpr = 1;
-        while (lpr < w4 && lpr < kWave) lpr *= 2;
-        const int rpw = kWave / lpr;
-        const dim3 grid((unsigned)ceil_div(rows, (int64_t)rpw * (kQuantThreads / kWave)));
-#define REEF_TOKEN_LAUNCH(L, P)                                                                \
-    hipLaunchKernelGGL((token_quantize_regs<L, P>), grid, dim3(kQuantThreads), 0, stream, x,   \
-                       rows, (int32_t)w4, row_stride, q, scales, status_word)
-        switch (lpr) {
-        case 1: REEF_TOKEN_LAUNCH(1, 1); break;
-        case 2: REEF_TOKEN_LAUNCH(2, 1); break;
-        case 4: REEF_TOKEN_LAUNCH(4, 1); break;
-        case 8: REEF_TOKEN_LAUNCH(8, 1); break;
-        case 16: REEF_TOKEN_LAUNCH(16, 1); break;
-        case 32: REEF_TOKEN_LAUNCH(32, 1); break;
-        default:
-            if (w4 <= kWave) REEF_TOKEN_LAUNCH(64, 1);
-            else if (w4 <= 2 * kWave) REEF_TOKEN_LAUNCH(64, 2);
-            else REEF_TOKEN_LAUNCH(64, 4);
-        }
-#undef REEF_TOKEN_LAUNCH
-    } else if (vec && w4 <= 8 * kQuantThreads && rows < (int64_t(1) << 31)) {
-        const dim3 grid((unsigned)rows);
-        if (w4 <= 2 * kQuantThreads)
-            hipLaunchKernelGGL(token_quantize_wide<2>, grid, dim3(kQuantThreads), 0, stream, x,
-                               (int32_t)w4, row_stride, q, scales, status_word);
-        else if (w4 <= 4 * kQuantThreads)
-            hipLaunchKernelGGL(token_quantize_wide<4>, grid, dim3(kQuantThreads), 0, stream, x,
-                               (int32_t)w4, row_stride, q, scales, status_word);
+    if (vec && (w4 <= 4 * kWave || (w4 <= 8 * kQuantThreads && rows < (int64_t(1) << 31)))) {
+        if (4 * rows * row_stride > kStreamBytes)
+            launch_rows<true>(x, rows, w4, row_stride, q, scales, status_word, stream);
         else
-            hipLaunchKernelGGL(token_quantize_wide<8>, grid, dim3(kQuantThreads), 0, stream, x,
-                               (int32_t)w4, row_stride, q, scales, status_word);
+            launch_rows<false>(x, rows, w4, row_stride, q, scales, status_word, stream);
     } else {
         const dim3 grid((unsigned)ceil_div(rows, kQuantThreads / kWave));
         hipLaunchKernelGGL(token_quantize, grid, dim3(kQuantThreads), 0, stream, x, rows, width,
@@ -670,12 +741,16 @@ extern "C" reef_status reef_dequantize_int8(const int8_t *q, int64_t n, int64_t 
     const int64_t groups = ceil_div(n, group);
     const int64_t blocks =
         std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(groups, kQuantThreads / tpr)));
-    if (vec)
-        hipLaunchKernelGGL(dequantize<true>, dim3((unsigned)blocks), dim3(kQuantThreads), 0, stream,
-                           q, n, group, tpr, scales, x);
+    const dim3 grid((unsigned)blocks);
+    if (vec && 4 * n > kStreamBytes)  // outputs no cache keeps: stored non-temporally
+        hipLaunchKernelGGL((dequantize<true, true>), grid, dim3(kQuantThreads), 0, stream, q, n,
+                           group, tpr, scales, x);
+    else if (vec)
+        hipLaunchKernelGGL((dequantize<true, false>), grid, dim3(kQuantThreads), 0, stream, q, n,
+                           group, tpr, scales, x);
     else
-        hipLaunchKernelGGL(dequantize<false>, dim3((unsigned)blocks), dim3(kQuantThreads), 0,
-                           stream, q, n, group, tpr, scales, x);
+        hipLaunchKernelGGL((dequantize<false, false>), grid, dim3(kQuantThreads), 0, stream, q, n,
+                           group, tpr, scales, x);
     return launch_status();
 }
 

@@ -177,6 +177,40 @@ def test_dequantize_bit_exact(reef, n, group):
     assert np.array_equal(x.view(np.uint32), want.view(np.uint32))
 
 
+def test_quantize_streams_beyond_the_cache(reef):
+    """537 MB of floats take the non-temporal streams (beyond the 256 MB last-level
+    cache; beyond 384 MB for the two-pass scales): per head, per tensor, per token
+    128 and 8192 wide, and a dequantize to 537 MB, bit-exact against the oracle."""
+    import torch
+    n = 4 * 32 * 8192 * 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(31)
+    xd = torch.randn(n, generator=g, device="cuda")
+    xd[::1_000_003] *= 40.0
+    x = host(xd)
+    case("quantize_per_head [4, 32, 8192, 128], 537 MB")
+    q, s = reef.quantize_per_head(xd.view(4, 32, 8192, 128))
+    qo, so = oracle.quantize_per_head(x.reshape(4, 32, 8192, 128))
+    assert np.array_equal(host(s).view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(host(q), qo)
+    case(f"quantize_per_tensor n={n}, 537 MB")
+    q, s = reef.quantize_per_tensor(xd)
+    qo, so = oracle.quantize_per_tensor(x)
+    assert host(s)[0].view(np.uint32) == so[0].view(np.uint32)
+    assert np.array_equal(host(q), qo)
+    for rows, width in ((1 << 20, 128), (16384, 8192)):
+        case(f"quantize_rows {rows}x{width}, 537 MB")
+        q, s = reef.quantize_rows(xd.view(rows, width))
+        qo, so = oracle.quantize_rows(x.reshape(rows, width))
+        assert np.array_equal(host(s).view(np.uint32), so.view(np.uint32))
+        assert np.array_equal(host(q), qo)
+    del qo, x
+    case(f"dequantize n={n} group=8192 to 537 MB")
+    out = host(reef.dequantize(q.reshape(-1), s, 8192))
+    want = oracle.dequantize(host(q), host(s), 8192)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+
+
 def test_quantize_rejects_non_finite(reef):
     case("quantize non-finite -> NonFiniteInput")
     for bad in (math.nan, math.inf, -math.inf):
