@@ -186,9 +186,10 @@ typedef struct reef_attention_params {
  *
  * workspace (optional, 256-byte aligned, at least
  * reef_attention_prefill_workspace_bytes(p) bytes; NULL/0 allowed) holds the
- * counters (a fixed 256 KB region, at most 65536 items of 128 query rows) and
- * partial results of the balanced schedule and, for head_dim 128, the fp16 value
- * image of the packed schedule (2 bytes per V element). It must be zero-filled
+ * counters (a fixed 256 KB region: the balanced schedule's, at most 65520 items of
+ * 128 query rows, and the packed schedule's item queue) and partial results of the
+ * balanced schedule and, for head_dim 128, the fp16 value image of the packed
+ * schedule (2 bytes per V element). It must be zero-filled
  * before its first use; every call leaves the counters zero-filled, and the
  * counters sit at the same offsets for every shape, so one workspace serves calls
  * of any shape that it is large enough for. Without it the library uses the

@@ -35,7 +35,8 @@ reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *
                                   const int64_t (&kst)[3], const int8_t *v,
                                   const int64_t (&vst)[3], const float *q_scales,
                                   const float *k_scales, const float *v_scales, float *out,
-                                  const int64_t (&ost)[3], void *image, hipStream_t stream);
+                                  const int64_t (&ost)[3], void *image, uint32_t *queue,
+                                  hipStream_t stream);
 
 namespace {
 
@@ -896,9 +897,11 @@ int64_t stream_groups() { return 2 * compute_units(); }
 // sized for head_dim 128. Counter i sits at the same place whatever the shape of
 // the call, and every launch leaves its counters at zero, so one zero-filled
 // workspace serves calls of any shape (the slots are written before they are read).
-constexpr int64_t kStreamMaxItems = 65536;
+constexpr int64_t kCounterWords = 65536;
+constexpr int64_t kQueueWords = 16;  // the last words: the packed schedule's item queue
+constexpr int64_t kStreamMaxItems = kCounterWords - kQueueWords;
 constexpr int64_t kStreamMinSteps = 8;  // steps per workgroup of the precise balanced kernels
-constexpr int64_t kStreamCounterBytes = kStreamMaxItems * 4;
+constexpr int64_t kStreamCounterBytes = kCounterWords * 4;
 
 int64_t stream_items(const reef_attention_params &p) {
     return ceil_div(p.q_len, kBM) * p.q_heads * p.batch;
@@ -1041,7 +1044,8 @@ extern "C" reef_status reef_attention_prefill_int8(
         const int64_t qst[3] = {a.q_sb, a.q_sh, a.q_st}, kst[3] = {a.k_sb, a.k_sh, a.k_st},
                       vst[3] = {a.v_sb, a.v_sh, a.v_st}, ost[3] = {a.o_sb, a.o_sh, a.o_st};
         return prefill_packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out,
-                                     ost, static_cast<char *>(workspace) + bal_bytes, stream);
+                                     ost, static_cast<char *>(workspace) + bal_bytes,
+                                     static_cast<uint32_t *>(workspace) + kStreamMaxItems, stream);
     }
     // The balanced schedule takes P split into hi + lo when the call asks for
     // precision (per-token K/V scales always do); without a request for precision the

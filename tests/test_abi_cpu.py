@@ -75,7 +75,7 @@ def test_prefill_workspace_bytes_and_alignment():
     lib = reef_amd.lib()
     p = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048)
     n = lib.reef_attention_prefill_workspace_bytes(C.byref(p))
-    # a fixed region of 65536 item counters, then two partial slots per workgroup, two
+    # a fixed region of 65536 counters (item counters and the packed queue), then two partial slots per workgroup, two
     # workgroups per compute unit (256 without a GPU): 128 x 128 outputs plus (max,
     # sum) of 128 rows; then the packed value image: 32 tiles of 64 keys per head,
     # 16 KB each, and one 4-byte block maximum per tile

@@ -638,23 +638,28 @@ def test_decode_paged_flags_bad_pages_and_lengths(reef):
 def test_workspaces_serve_calls_of_any_shape(reef):
     """One zero-filled workspace reused by calls of different shapes: the balanced
     prefill with 48 items and then 96 (a layout with a per-call number of counters
-    made the second call read the first call's part slots as counters), and decode
-    with 8 items and then 80. The counters sit at fixed offsets, so every call
-    matches the oracle."""
-    big = reef.AttentionParams(2, 16, 4, 300, 1000, 64, 700, 0, 0.125, 1, 1, 0)
+    made the second call read the first call's part slots as counters), the packed
+    prefill (whose item queue sits in the last words of the same counter region)
+    between them, and decode with 8 items and then 80. The counters sit at fixed
+    offsets and every call leaves them zero, so every call matches the oracle."""
+    big = reef.AttentionParams(2, 16, 4, 300, 1000, 128, 700, 0, 0.125, 1, 1, 0)
     ws = torch.zeros(reef.lib().reef_attention_prefill_workspace_bytes(reef.C.byref(big)),
                      dtype=torch.uint8, device="cuda")
-    for B in (1, 2, 1, 2):
-        case(f"prefill balanced B{B} Hq16 Hkv4 Sq300 Skv1000 D64, one workspace")
-        seed = 400 + B
-        q = W.lcg_normal(seed, B * 16 * 300 * 64).reshape(B, 16, 300, 64)
-        k = W.lcg_normal(seed + 1, B * 4 * 1000 * 64).reshape(B, 4, 1000, 64)
-        v = W.lcg_normal(seed + 2, B * 4 * 1000 * 64).reshape(B, 4, 1000, 64)
-        p = oracle.Problem(B, 16, 4, 300, 1000, 64, softmax_scale=0.125)
-        out, gold = _run_prefill(reef, q, k, v, p, workspace=ws, schedule=reef.SCHED_BALANCED)
+    counters = 65536 * 4
+    for B, D, sched in ((1, 64, "BALANCED"), (2, 128, "PACKED"), (2, 64, "BALANCED"),
+                        (1, 128, "PACKED"), (1, 64, "BALANCED"), (2, 64, "BALANCED")):
+        case(f"prefill {sched.lower()} B{B} Hq16 Hkv4 Sq300 Skv1000 D{D}, one workspace")
+        seed = 400 + B + D
+        q = W.lcg_normal(seed, B * 16 * 300 * D).reshape(B, 16, 300, D)
+        k = W.lcg_normal(seed + 1, B * 4 * 1000 * D).reshape(B, 4, 1000, D)
+        v = W.lcg_normal(seed + 2, B * 4 * 1000 * D).reshape(B, 4, 1000, D)
+        p = oracle.Problem(B, 16, 4, 300, 1000, D, softmax_scale=0.125)
+        out, gold = _run_prefill(reef, q, k, v, p, workspace=ws,
+                                 schedule=getattr(reef, "SCHED_" + sched))
         err = np.abs(out - gold).max()
         print(f"max_abs_err {err:.3e}", flush=True)
         assert err <= TOL
+        assert not ws[:counters].any(), "a call left counters behind"
     D, Hq, Hkv = 128, 8, 2
     dbig = reef.DecodeParams(40, Hq, Hkv, D, 640, 0, 1 / math.sqrt(D), reef.PER_TOKEN, 0, 0)
     dws = reef.decode_workspace(dbig, "cuda")
