@@ -27,11 +27,11 @@
 //     activation-outlier channels of int8 LLM attention (|v| ~ 30) need the split.
 //     Each block keeps the row sum of exactly the P values its product uses.
 //   * Schedule: persistent workgroups; a causal head's query tiles t and T-1-t form
-//     one item with the same number of key tiles as any other pair. Items are
-//     numbered head-major; each XCD owns an eighth of them (a few heads at a time,
-//     whose K and V stay in that XCD's L2) in a queue its workgroups take from as
-//     they finish, then the other XCDs' queues. The light tile runs first: its keys
-//     are a prefix of the heavy one's.
+//     one unit with the same number of key tiles as any other pair. Each XCD owns
+//     an eighth of the heads (a few at a time, whose K and V stay in that XCD's L2)
+//     in a queue its workgroups take from as they finish, then the other XCDs'
+//     queues; the last heads of a share come as single tiles, heaviest first. The
+//     light tile of a pair runs first: its keys are a prefix of the heavy one's.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -591,44 +591,74 @@ __device__ __forceinline__ uint32_t precise_blocks(const PackedArgs &a, int b, i
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)mask);
 }
 
+// XCD y's share of the work: the (batch, head) pairs [bh0, bh0 + nh), an eighth of
+// them (a few consecutive heads, whose K and V stay in the XCD's L2). Its units: the
+// query-tile pairs of the first nh - tail heads, then the single query tiles of the
+// last `tail` heads, heaviest first, so that the last units of a launch are short.
+struct Share {
+    int bh0, nh, tail, pairs, units;
+};
+__device__ __forceinline__ Share share_of(const PackedArgs &a, int y) {
+    const int64_t bh_total = (int64_t)a.batch * a.q_heads;
+    const int wgs = max(1, (int)gridDim.x / kXcdCount);
+    Share s;
+    s.bh0 = (int)(bh_total * y / kXcdCount);
+    s.nh = (int)(bh_total * (y + 1) / kXcdCount) - s.bh0;
+    s.tail = min(s.nh, (2 * wgs + a.q_tiles - 1) / a.q_tiles);  // about two tiles per workgroup
+    s.pairs = (s.nh - s.tail) * a.per_head;
+    s.units = s.pairs + s.tail * a.q_tiles;
+    return s;
+}
+
 // Two workgroups per compute unit: the two waves on each SIMD belong to different
-// workgroups and fill each other's waits. Items are taken from a queue per XCD:
-// XCD x owns the x-th eighth of the items (a few consecutive heads, whose K and V
-// stay in its L2), its workgroups take them in order as they finish the previous
-// one, and a workgroup whose XCD has none left takes from the other XCDs' queues.
-// Items differ in cost (the hi + lo products of a head's precise value blocks):
-// with items dealt out in a fixed order the last workgroups ended 15 % after the
-// mean (4x32x8192x128: 2.30 ms dealt out, 2.18-2.19 ms from the queues). The last
-// workgroup to finish resets the queue to zero for the next call.
+// workgroups and fill each other's waits. Units are taken from a queue per XCD (its
+// share above, in order, as the workgroups finish the previous one), then from the
+// other XCDs' queues. Units differ in cost (the hi + lo products of a head's precise
+// value blocks, and the single tiles): with pairs dealt out in a fixed order the
+// last workgroups ended 15 % after the mean (4x32x8192x128: 2.30 ms dealt out,
+// 2.18-2.19 ms from the queues of pairs, whose last workgroups still ended 7 %
+// after the mean; with the single tiles last 3 %, 1 % faster). The last workgroup
+// to finish resets the queue to zero for the next call.
 __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(PackedArgs a) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[kKRing + kVRing];
     __shared__ uint32_t sRed[4 * kWaves];
-    __shared__ int sItem;
+    __shared__ int sUnit[2];  // XCD share and unit, or -1
     const int x = blockIdx.x % kXcdCount;
     int tried = 0;  // queues found empty, own XCD's first
-    auto take = [&]() -> int {  // thread 0: the next item, or -1 when every queue is empty
+    auto take = [&](int &share) -> int {  // thread 0: the next unit, or -1 when all are taken
         while (tried < kXcdCount) {
-            const int y = (x + tried) % kXcdCount;
-            const int lo = (int)((int64_t)a.items * y / kXcdCount);
-            const int hi = (int)((int64_t)a.items * (y + 1) / kXcdCount);
-            const uint32_t n = __hip_atomic_fetch_add(a.queue + y, 1u, __ATOMIC_RELAXED,
+            share = (x + tried) % kXcdCount;
+            const uint32_t n = __hip_atomic_fetch_add(a.queue + share, 1u, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT);
-            if ((int64_t)lo + n < hi) return lo + (int)n;
+            if ((int64_t)n < share_of(a, share).units) return (int)n;
             ++tried;
         }
         return -1;
     };
     for (;;) {
-        if (threadIdx.x == 0) sItem = take();
+        if (threadIdx.x == 0) {
+            int share = 0;
+            sUnit[1] = take(share);
+            sUnit[0] = share;
+        }
         __syncthreads();
-        const int it = sItem;
-        __syncthreads();  // every thread has read sItem before thread 0 writes it again
-        if (it < 0) break;
-        const int bh = it / a.per_head, i = it % a.per_head;
+        const int y = sUnit[0], u = sUnit[1];
+        __syncthreads();  // every thread has read sUnit before thread 0 writes it again
+        if (u < 0) break;
+        const Share s = share_of(a, y);
+        int bh, first, second = -1;
+        if (u < s.pairs) {
+            bh = s.bh0 + u / a.per_head;
+            first = u % a.per_head;                 // the light tile, whose keys are a prefix
+            if (a.q_tiles - 1 - first != first) second = a.q_tiles - 1 - first;  // of the heavy's
+        } else {
+            const int v = u - s.pairs;
+            bh = s.bh0 + (s.nh - s.tail) + v % s.tail;
+            first = a.q_tiles - 1 - v / s.tail;
+        }
         const int b = bh / a.q_heads, h = bh % a.q_heads;
         const int kvh = h / (a.q_heads / a.kv_heads);
         const uint32_t pmask = precise_blocks(a, b, kvh, sRed);
-        const int light = i, heavy = a.q_tiles - 1 - i;
         // Scores read as biased floats need the biased maximum's rounding (half an
         // ulp of 12582912 c) well below the lazy-rescale margin: c <= 4 (any q
         // scale granularity but per token, where c varies by row).
@@ -639,8 +669,8 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(Pac
                 4.0f;
         auto run = [&](auto lo_tag, auto bias_tag) {
             constexpr bool LO = decltype(lo_tag)::value, BIAS = decltype(bias_tag)::value;
-            packed_tile<LO, BIAS>(a, b, h, light, smem, pmask);
-            if (heavy != light) packed_tile<LO, BIAS>(a, b, h, heavy, smem, pmask);
+            packed_tile<LO, BIAS>(a, b, h, first, smem, pmask);
+            if (second >= 0) packed_tile<LO, BIAS>(a, b, h, second, smem, pmask);
         };
         if (pmask) {
             if (biased) run(std::true_type{}, std::true_type{});
