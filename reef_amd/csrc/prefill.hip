@@ -621,11 +621,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     }
     if (MODE == kStream && sp.parts > 1) {
         // Leave this part in its slot (every lane: rows past q_len hold finite
-        // values), then count the part in; the last part of the item merges. The
-        // slot stores and loads are device-coherent atomics (sc1); every thread
-        // releases its stores at agent scope before the barrier, the counter
-        // increment is an acquire-release operation, and the merging part acquires
-        // at agent scope before it reads the other parts' slots.
+        // values), then count the part in; the last part of the item merges. Every
+        // access to a slot is a device-coherent atomic (agent scope: written through
+        // to, and read from, the memory side beneath the per-XCD L2s); each thread
+        // waits until its slot stores have completed before the barrier that
+        // precedes the count, and the merging part reads the slots only after its
+        // count returned. The same protocol as the decode merge. Release and acquire
+        // fences at agent scope compile to a write-back and an invalidation of the
+        // whole XCD L2 (buffer_wbl2 / buffer_inv), which every other workgroup on
+        // the XCD then pays in K and V misses: 106 against 57 us on 1x32x2048x128.
         constexpr int SF = StreamSlot<D>::FLOATS, OF = StreamSlot<D>::O_FLOATS;
         constexpr int E = DB * 8;  // 8-byte elements of output per lane
         auto pack = [](float x, float y) {
@@ -648,14 +652,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                 put(so + (wave * E + d * 8 + e) * kWave + lane,
                     pack(acc[d][2 * e], acc[d][2 * e + 1]));
         put(so + OF / 2 + wave * kWave + lane, pack(m_run, l_tot));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);  // vmcnt 0: every slot store has completed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __syncthreads();
         if (tid == 0)
-            *sTicket = __hip_atomic_fetch_add(sa.counters + sp.item, 1u, __ATOMIC_ACQ_REL,
+            *sTicket = __hip_atomic_fetch_add(sa.counters + sp.item, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (*sTicket != (uint32_t)(sp.parts - 1)) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (tid == 0)  // ready for the next launch
             __hip_atomic_store(sa.counters + sp.item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // Parts in order: part p is workgroup first_wg + p; the first part sits in
@@ -814,8 +820,12 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
         sp.parts = wg_of(sp.item_u0 + n - 1) - sp.first_wg + 1;
         sp.slot = 2 * L + (first ? 0 : 1);
         sp.item = bh * a.q_tiles + tile;
-        prefill_body<D, KV_TOKEN, PRECISE, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0,
-                                                    c1, smem, sScale, sa, sp, &sTicket);
+        // With item_sel, one launch takes the items whose values need hi + lo P and
+        // another the rest; each walks the same ranges and skips the other's items.
+        if (KV_TOKEN || a.item_sel == 0 ||
+            item_is_wide(a, bh / a.q_heads, bh % a.q_heads) == (a.item_sel == 2))
+            prefill_body<D, KV_TOKEN, PRECISE, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads,
+                                                        c0, c1, smem, sScale, sa, sp, &sTicket);
         u += c1 - c0;
         c0 = 0;
         first = false;
@@ -1047,21 +1057,22 @@ extern "C" reef_status reef_attention_prefill_int8(
                                      ost, static_cast<char *>(workspace) + bal_bytes,
                                      static_cast<uint32_t *>(workspace) + kStreamMaxItems, stream);
     }
-    // The balanced schedule takes P split into hi + lo when the call asks for
-    // precision (per-token K/V scales always do); without a request for precision the
-    // library leaves it to callers that force it. With precision and fewer 128-row
-    // tiles than compute units (a short chunk of queries over a long cache), the
-    // library takes it: the one-item kernel would leave most of the GPU idle. The
-    // split and one-item kernels split P where the values need it (per item, two
-    // launches); with at most one item per compute unit the library takes the split
-    // kernel, whose key split is the only parallelism left to balance the causal work
-    // (1x8q/1kv x4096x128: 67 against 82 us); with more, two one-item workgroups per
-    // compute unit overlap each other's prologue and epilogue better.
+    // Every schedule splits P into hi + lo where the values need it: always with the
+    // precision flag or per-token K/V scales, otherwise per item (two launches, each
+    // skipping the other's items). The library takes the balanced schedule, which
+    // cuts the causal work of all items into equal ranges, for grids of at most one
+    // 128-row tile per compute unit (1x8q/1kv x4096x128: 54 against 70 us with the
+    // split kernel and 82 us with the one-item kernel; with precision, fewer tiles
+    // than units: a short chunk of queries over a long cache); with more tiles, two
+    // one-item workgroups per compute unit do as well (1x32x2048x128: 54 against 57
+    // us balanced). Without a workspace small grids take the split kernel, whose key
+    // split is the only parallelism left to balance the causal work.
     if (sched == REEF_ATTN_SCHED_BALANCED && !stream_ok) return REEF_INVALID_ARGUMENT;
     if (sched == REEF_ATTN_SCHED_SPLIT && tok) return REEF_INVALID_ARGUMENT;
     a.item_sel = 0;
     if (sched == REEF_ATTN_SCHED_BALANCED ||
-        (sched == REEF_ATTN_SCHED_AUTO && precise && stream_ok && items < compute_units())) {
+        (sched == REEF_ATTN_SCHED_AUTO && stream_ok &&
+         (precise ? items < compute_units() : items <= compute_units()))) {
         const int64_t per_head = host_steps_before(*p, a.q_tiles - 1) +
                                  host_tile_steps(*p, a.q_tiles - 1);
         StreamArgs sa;
@@ -1076,23 +1087,35 @@ extern "C" reef_status reef_attention_prefill_int8(
         // unit, so that every workgroup runs at once, and at least kStreamMinSteps
         // steps per workgroup, so that a short chunk of queries over a long prefix is
         // cut into a few parts per item (each merge reads its parts one after another).
-        const int64_t groups =
-            (tok || precise) ? std::max<int64_t>(1, std::min<int64_t>(compute_units(),
-                                                                      sa.units / kStreamMinSteps))
-                             : stream_groups();
-        const dim3 sgrid((unsigned)std::min<int64_t>(groups, sa.units));
+        auto grid_of = [&](bool prec) {
+            const int64_t groups =
+                prec ? std::max<int64_t>(1, std::min<int64_t>(compute_units(),
+                                                              sa.units / kStreamMinSteps))
+                     : stream_groups();
+            return dim3((unsigned)std::min<int64_t>(groups, sa.units));
+        };
 #define REEF_STREAM_LAUNCH(DIM, TOK, PREC)                                                   \
-    hipLaunchKernelGGL((prefill_stream_kernel<DIM, TOK, PREC>), sgrid, dim3(kThreads), 0, stream, \
-                       a, sa)
-        if (D == 128) {
-            if (tok) REEF_STREAM_LAUNCH(128, true, true);
-            else if (precise) REEF_STREAM_LAUNCH(128, false, true);
-            else REEF_STREAM_LAUNCH(128, false, false);
-        } else {
-            if (tok) REEF_STREAM_LAUNCH(64, true, true);
-            else if (precise) REEF_STREAM_LAUNCH(64, false, true);
-            else REEF_STREAM_LAUNCH(64, false, false);
+    hipLaunchKernelGGL((prefill_stream_kernel<DIM, TOK, PREC>), grid_of(PREC), dim3(kThreads), \
+                       0, stream, a, sa)
+        if (precise) {
+            if (D == 128) {
+                if (tok) REEF_STREAM_LAUNCH(128, true, true);
+                else REEF_STREAM_LAUNCH(128, false, true);
+            } else {
+                if (tok) REEF_STREAM_LAUNCH(64, true, true);
+                else REEF_STREAM_LAUNCH(64, false, true);
+            }
+            return launch_status();
         }
+        // Items whose values stay within kPreciseAbove take one fp16 P, the others the
+        // hi + lo split (the precise kernel's grid); each launch skips the other's items.
+        a.item_sel = 1;
+        if (D == 128) REEF_STREAM_LAUNCH(128, false, false);
+        else REEF_STREAM_LAUNCH(64, false, false);
+        if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
+        a.item_sel = 2;
+        if (D == 128) REEF_STREAM_LAUNCH(128, false, true);
+        else REEF_STREAM_LAUNCH(64, false, true);
 #undef REEF_STREAM_LAUNCH
         return launch_status();
     }

@@ -319,9 +319,10 @@ def test_prefill_matches_oracle(reef, B, Hq, Hkv, Sq, Skv, D, start, window, gq,
 def test_prefill_outlier_channels(reef):
     """Per-head scales with a few value channels scaled x8 (activation outliers):
     the values of those heads reach |v| ~ 30, where one fp16 P is not precise enough.
-    Every schedule the library chooses by itself (packed with a workspace, the
-    one-item kernel without), the forced precise one-item kernel and the forced split
-    kernel (hi + lo P on the outlier heads) stay within TOL."""
+    Every schedule the library chooses by itself (balanced with a workspace, 36 tiles
+    on 256 compute units; the split kernel without), the forced packed and one-item
+    kernels, the forced precise one-item kernel and the forced split and balanced
+    schedules (hi + lo P on the outlier heads) stay within TOL."""
     B, H, S, D = 1, 4, 1100, 128
     case(f"prefill outlier channels B{B} H{H} S{S} D{D}")
     q = W.lcg_normal(801, B * H * S * D).reshape(B, H, S, D)
@@ -333,7 +334,8 @@ def test_prefill_outlier_channels(reef):
     p = oracle.Problem(B, H, H, S, S, D, softmax_scale=1 / math.sqrt(D))
     runs = [(False, reef.SCHED_AUTO, None), (False, reef.SCHED_AUTO, False),
             (False, reef.SCHED_PACKED, None), (False, reef.SCHED_ONE_ITEM, False),
-            (True, reef.SCHED_ONE_ITEM, False), (False, reef.SCHED_SPLIT, False)]
+            (True, reef.SCHED_ONE_ITEM, False), (False, reef.SCHED_SPLIT, False),
+            (False, reef.SCHED_BALANCED, None)]
     for precise, sched, ws in runs:
         out, gold = _run_prefill(reef, q, k, v, p, precise, workspace=ws, schedule=sched)
         err = np.abs(out - gold).max()
