@@ -148,10 +148,12 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
  * tune it and for tests that must reach every path. A forced schedule that the
  * call cannot use (BALANCED without a large enough workspace, SPLIT with PER_TOKEN
  * K/V scales, PACKED without head_dim 128, per-tensor or per-head K/V scales and a
- * workspace) returns REEF_INVALID_ARGUMENT. AUTO takes BALANCED for a call with
- * PRECISE_PV or PER_TOKEN K/V scales, a large enough workspace and fewer 128-row
- * query tiles than compute units, and SPLIT for other calls with at most one such
- * tile per compute unit. */
+ * workspace) returns REEF_INVALID_ARGUMENT. AUTO takes PACKED for head_dim 128 with
+ * at least one pair of 256-row query tiles per compute unit (and a workspace that
+ * holds the image); BALANCED with a large enough workspace and at most one 128-row
+ * query tile per compute unit (fewer than one with PRECISE_PV or PER_TOKEN K/V
+ * scales); without a workspace SPLIT for those small grids; ONE_ITEM otherwise.
+ * Every schedule splits P into hi + lo where the values need it. */
 #define REEF_ATTN_SCHED_MASK 0x70u
 #define REEF_ATTN_SCHED_AUTO 0x00u
 #define REEF_ATTN_SCHED_ONE_ITEM 0x10u /* one 128-row query tile per workgroup */
@@ -160,11 +162,13 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
                                         * need it or with PRECISE_PV */
 #define REEF_ATTN_SCHED_BALANCED 0x30u /* equal (tile, key block) ranges per workgroup;
                                         * cut tiles merge through the workspace; hi + lo
-                                        * P with PRECISE_PV or PER_TOKEN K/V scales */
+                                        * P where the values need it or with PRECISE_PV
+                                        * or PER_TOKEN K/V scales */
 #define REEF_ATTN_SCHED_PACKED 0x40u   /* head_dim 128, per-tensor / per-head K and V
                                         * scales: V packed once into an fp16 image in the
-                                        * workspace, 256-row query tiles, persistent
-                                        * workgroups over (light, heavy) tile pairs */
+                                        * workspace, 128-row query tiles, persistent
+                                        * workgroups taking (light, heavy) tile pairs
+                                        * from per-XCD queues in the workspace */
 
 typedef struct reef_attention_params {
     int64_t batch, q_heads, kv_heads; /* q head h reads kv head h / (q_heads / kv_heads) */
