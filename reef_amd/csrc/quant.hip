@@ -37,6 +37,38 @@ __device__ __forceinline__ float4 load4(const float4 *p) {
     }
 }
 
+// Codes of quantize_int8 for a group of values that share one scale, from
+// y = x * rcp(scale) instead of the IEEE quotient t = x / scale: |x| <= 127 scale
+// bounds |t| by 127 (1 + 2^-24); rcp is within 1 ulp and the product is rounded
+// once, so |y - t| < 2^-15.4, and t's own rounding adds under 2^-16.9: y lies
+// within 3.1e-5 of the engine's quotient. Unless y is within 2^-14 of a
+// half-integer, rint(y) is the engine's code. When any lane of the wave has such
+// a value (about 1.2e-4 per value), or the scale is below 2^-125 or not finite,
+// the active lanes of the wave take IEEE quotients for the whole group (one
+// ballot; lanes that do not call it take no part).
+template <int N>
+__device__ __forceinline__ void quantize_group(const float (&x)[N], float scale,
+                                               int8_t (&code)[N]) {
+    const float rs = __builtin_amdgcn_rcpf(scale);
+    bool near = !(scale >= 0x1p-125f && scale <= 3.4028235e38f);
+    float r[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float y = x[i] * rs;
+        r[i] = __builtin_rintf(y);
+        near |= __builtin_fabsf(y - r[i]) > 0.5f - 0x1p-14f;
+    }
+    if (__builtin_amdgcn_ballot_w64(near) != 0) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) r[i] = __builtin_rintf(x[i] / scale);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float c = r[i] < -127.0f ? -127.0f : (r[i] > 127.0f ? 127.0f : r[i]);
+        code[i] = (int8_t)(int)c;
+    }
+}
+
 // Largest magnitudes are reduced as the bit patterns of |x|: for non-negative
 // floats the unsigned order of the bits is the float order, and any Inf or NaN
 // (>= 0x7f800000) wins, which the quantize pass reports as non-finite input.
@@ -333,18 +365,22 @@ __global__ __launch_bounds__(kQuantThreads) void head_quantize_flat(FlatHeads f,
             const int64_t j = i + u * kQuantThreads;
             v[u] = j < i1 ? load4<NT>(x + j) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        float xs[4 * kFlatUnroll];
+#pragma unroll
+        for (int u = 0; u < kFlatUnroll; ++u) {
+            bad |= !(__builtin_isfinite(v[u].x) && __builtin_isfinite(v[u].y) &&
+                     __builtin_isfinite(v[u].z) && __builtin_isfinite(v[u].w));
+            xs[4 * u] = v[u].x;
+            xs[4 * u + 1] = v[u].y;
+            xs[4 * u + 2] = v[u].z;
+            xs[4 * u + 3] = v[u].w;
+        }
+        int8_t c[4 * kFlatUnroll];
+        quantize_group(xs, scale, c);  // the lanes past i1 hold zeros
 #pragma unroll
         for (int u = 0; u < kFlatUnroll; ++u) {
             const int64_t j = i + u * kQuantThreads;
-            if (j >= i1) break;
-            bad |= !(__builtin_isfinite(v[u].x) && __builtin_isfinite(v[u].y) &&
-                     __builtin_isfinite(v[u].z) && __builtin_isfinite(v[u].w));
-            char4 c;
-            c.x = quantize_int8(v[u].x, scale);
-            c.y = quantize_int8(v[u].y, scale);
-            c.z = quantize_int8(v[u].z, scale);
-            c.w = quantize_int8(v[u].w, scale);
-            out[j] = c;
+            if (j < i1) out[j] = char4{c[4 * u], c[4 * u + 1], c[4 * u + 2], c[4 * u + 3]};
         }
     }
     if (bad) flag_status(status, REEF_STATUS_BIT_NON_FINITE);
@@ -402,19 +438,22 @@ __global__ __launch_bounds__(kQuantThreads) void token_quantize_regs(
             m = m > w ? m : w;
         }
         const float scale = int8_scale(__uint_as_float(m));
+        float xs[4 * PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            xs[4 * j] = v[g][j].x;
+            xs[4 * j + 1] = v[g][j].y;
+            xs[4 * j + 2] = v[g][j].z;
+            xs[4 * j + 3] = v[g][j].w;
+        }
+        int8_t c[4 * PER];
+        quantize_group(xs, scale, c);
         if (row < rows) {
             char4 *out = reinterpret_cast<char4 *>(q + row * (int64_t)w4 * 4);
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
                 const int col = l + j * LPR;
-                if (col < w4) {
-                    char4 c;
-                    c.x = quantize_int8(v[g][j].x, scale);
-                    c.y = quantize_int8(v[g][j].y, scale);
-                    c.z = quantize_int8(v[g][j].z, scale);
-                    c.w = quantize_int8(v[g][j].w, scale);
-                    out[col] = c;
-                }
+                if (col < w4) out[col] = char4{c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]};
             }
             if (l == 0) {
                 scales[row] = scale;
@@ -452,18 +491,21 @@ __global__ __launch_bounds__(kQuantThreads) void token_quantize_wide(
 #pragma unroll
     for (int w = 0; w < kQuantThreads / kWave; ++w) m = m > partial[w] ? m : partial[w];
     const float scale = int8_scale(__uint_as_float(m));
+    float xs[4 * PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        xs[4 * j] = v[j].x;
+        xs[4 * j + 1] = v[j].y;
+        xs[4 * j + 2] = v[j].z;
+        xs[4 * j + 3] = v[j].w;
+    }
+    int8_t c[4 * PER];
+    quantize_group(xs, scale, c);
     char4 *out = reinterpret_cast<char4 *>(q + row * (int64_t)w4 * 4);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int col = threadIdx.x + j * kQuantThreads;
-        if (col < w4) {
-            char4 c;
-            c.x = quantize_int8(v[j].x, scale);
-            c.y = quantize_int8(v[j].y, scale);
-            c.z = quantize_int8(v[j].z, scale);
-            c.w = quantize_int8(v[j].w, scale);
-            out[col] = c;
-        }
+        if (col < w4) out[col] = char4{c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]};
     }
     if (threadIdx.x == 0) {
         scales[row] = scale;
