@@ -22,8 +22,11 @@
 //     softmax so the matrix cores and the vector ALU work side by side.
 //   * Precision of P: for a value block whose dequantized magnitudes reach above
 //     kPreciseAbove, P is split into fp16 hi + lo parts (two products, 22 bits);
-//     below it, P is one fp16 (11 bits). The rounding of P moves an output by about
-//     2^-12 |v_j - out| per dominant key, which at |v| <= 6 stays under 5e-4; the
+//     below it, P is one fp16 (11 bits). Each P is then off by at most 2^-11 of
+//     itself, so an output by at most 2^-11 max|v_j - out|; when many keys share
+//     the weight the roundings mostly cancel (under 5.4e-4 on the benchmark
+//     workloads at |v| <= 6), but two dominant keys of values +-6 can move an
+//     output by 1.2e-3 (REEF_ATTN_PRECISE_PV splits every block). The
 //     activation-outlier channels of int8 LLM attention (|v| ~ 30) need the split.
 //     Each block keeps the row sum of exactly the P values its product uses.
 //   * Schedule: persistent workgroups; a causal head's query tiles t and T-1-t form

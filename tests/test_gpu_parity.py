@@ -344,6 +344,44 @@ def test_prefill_outlier_channels(reef):
         assert err <= TOL, (precise, sched, ws, err)
 
 
+def test_prefill_two_key_rounding_of_p(reef):
+    """The rounding of one fp16 P in its worst case: row 1 sees two keys with values
+    +6 and -6 in every channel (127 s_v = 6, the largest magnitude that keeps one
+    fp16 P) and the weight ratio r = 0.5 + 0.9 2^-12, which fp16 rounds to 0.5,
+    moving the output by 0.9 2^-12 * 12 / (1 + r)^2 = 1.17e-3, past the 1e-3 of the
+    attention tolerance. With REEF_ATTN_PRECISE_PV (P = hi + lo) every schedule
+    stays within 1e-5 of the oracle; without it, the error stays below the bound
+    2^-11 max|v_j - out| of one fp16 P (each P relative to 2^-11)."""
+    D = 128
+    case("prefill two-key row, fp16 rounding of P at its worst")
+    q = np.ones((1, 1, 2, D), np.int8)
+    k = np.zeros((1, 1, 2, D), np.int8)
+    k[0, 0, 1] = -8                                   # s0 - s1 = 1024
+    v = np.empty((1, 1, 2, D), np.int8)
+    v[0, 0, 0], v[0, 0, 1] = 127, -127
+    qs = np.ones(1, np.float32)
+    ks = np.ones(1, np.float32)
+    vs = np.full(1, 6.0 / 127.0, np.float32)
+    r = 0.5 + 0.9 * 2.0 ** -12
+    scale = math.log(1.0 / r) / 1024.0
+    p = oracle.Problem(1, 1, 1, 2, 2, D, softmax_scale=scale, q_granularity=1,
+                       kv_granularity=1)
+    gold = oracle.attention_int8(p, q, k, v, qs, ks, vs)
+    assert abs(gold[0, 0, 1, 0] - 6.0 * (1 - r) / (1 + r)) < 1e-5
+    spread = float(np.abs(6.0 - gold[0, 0, 1]).max())  # max |v_j - out| of row 1
+    for precise in (True, False):
+        for sched in (reef.SCHED_AUTO, reef.SCHED_ONE_ITEM, reef.SCHED_SPLIT,
+                      reef.SCHED_BALANCED, reef.SCHED_PACKED):
+            out = reef.attention_prefill(gpu(q), gpu(k), gpu(v), gpu(qs), gpu(ks), gpu(vs),
+                                         softmax_scale=scale, precise=precise, schedule=sched)
+            err = float(np.abs(host(out) - gold).max())
+            print(f"precise={precise} schedule={sched:#x} max_abs_err {err:.3e}", flush=True)
+            if precise:
+                assert err <= 1e-5, (sched, err)
+            else:
+                assert err <= 2.0 ** -11 * spread, (sched, err)
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,S,D,gran", [(1, 8, 2, 300, 128, 1), (2, 4, 4, 130, 64, 0),
                                                (1, 4, 1, 77, 128, 2)])
 def test_prefill_projection_layout_strides(reef, B, Hq, Hkv, S, D, gran):
