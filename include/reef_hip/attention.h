@@ -141,15 +141,15 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
  */
 
 /* Attention flags. */
-#define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts in every
-                                     * value block (always on with PER_TOKEN K/V
-                                     * scales): outputs within 1e-3 of the fp32
-                                     * reference for any input. Without it, blocks whose
-                                     * dequantized values stay within 6 round P once to
-                                     * fp16: within 1e-3 on attention over many keys,
-                                     * but up to 2^-11 max|v_j - out| (1.2e-3 seen) on
-                                     * rows where two keys of opposite values carry the
-                                     * weight */
+#define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts (22
+                                     * bits) whatever the values. Without it the split
+                                     * applies wherever a head's dequantized values reach
+                                     * above 1 in magnitude (always with PER_TOKEN K/V
+                                     * scales); at or below 1 one fp16 P moves an output
+                                     * by at most 2^-11 max|v_j - out| <= 9.8e-4. Either
+                                     * way each P carries an exponent offset that keeps
+                                     * it out of the fp16 subnormals, so small weights
+                                     * keep their precision */
 /* Prefill work schedule (bits 4-6 of flags). AUTO lets the library choose from the
  * grid size and the workspace; the others force one schedule, for callers that
  * tune it and for tests that must reach every path. A forced schedule that the

@@ -264,15 +264,17 @@ __device__ __forceinline__ void block_math(const DecodeBlock<D> &cur, int kb, in
     vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
 
     // Lazy rescale: the running max moves only when a head's block max exceeds
-    // it by more than 2^8, and the value normalizer s_run (values accumulate in
-    // units of s_run, the largest value scale so far) only when a value scale
-    // exceeds it 16-fold, so p * v_scale / s_run stays below 2^12 in fp16.
-    if (__any(mt > st.m_run + 8.0f || vmax > st.s_run * 16.0f)) {
+    // it by more than 2^6, and the value normalizer s_run (values accumulate in
+    // units of s_run / 2^8, s_run the largest value scale so far) only when a value
+    // scale exceeds it 2-fold, so the weight p * v_scale * 2^8 / s_run stays below
+    // 2^15 in fp16, and above its subnormals (hi and lo keep 11 bits each) wherever
+    // its share of the row sum (of p itself) exceeds 2^-21.
+    if (__any(mt > st.m_run + 6.0f || vmax > st.s_run * 2.0f)) {
         const float m_new = fmaxf(st.m_run, mt);
         const float s_new = fmaxf(st.s_run, vmax);
         const float alpha = st.m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m_run - m_new);
         const float alpha_o = s_new > 0.0f ? alpha * (st.s_run / s_new) : alpha;
-        st.inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
+        st.inv_s = s_new > 0.0f ? 256.0f / s_new : 0.0f;
         st.m_run = m_new;
         st.s_run = s_new;
         st.l_run *= alpha;
@@ -547,7 +549,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, PAGED ? kWgPerCu : 1) void decod
         float m = st.m_run;
         f32x4 o[DB];
 #pragma unroll
-        for (int d = 0; d < DB; ++d) o[d] = st.acc[d] * st.s_run;
+        for (int d = 0; d < DB; ++d) o[d] = st.acc[d] * (st.s_run * (1.0f / 256.0f));
         merge_waves<D>(m, l, o, sO, sML, wave, lane);
 
         // Workgroups holding a part of this item: the non-empty ones in gf .. gl.

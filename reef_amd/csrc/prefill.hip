@@ -57,7 +57,7 @@ struct PrefillArgs {
     int32_t q_tiles;
     int32_t zigzag;  // pair heavy and light tiles in grids that fit at once
     // Items this launch computes (per-tensor / per-head K/V scales): 0 all, 1 those
-    // whose largest dequantized value 127 s_v is at most kPreciseAbove, 2 the others.
+    // whose largest dequantized value 127 s_v is at most kHiOnlyMax, 2 the others.
     int32_t item_sel;
 };
 
@@ -257,6 +257,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     constexpr int KLOADS = kBN * D / 16 / kThreads;  // 16-byte K loads per thread
     constexpr int VBLOCKS = (kBN / 4) * (D / 8);     // 4-key x 8-channel V blocks
     constexpr float kLazy = 8.0f;  // rescale only when a row max grows by > 2^8
+    // p = exp2(s - m_run + kShift): the row sums and the merges carry the same factor
+    // 2^kShift, which cancels; it keeps a p of weight above 2^-21 of the row's
+    // largest out of the fp16 subnormals (so hi and lo keep 11 bits each; below, each
+    // p is off by at most 2^-25, under 2^-32 of the row sum), and every p below
+    // 2^(kLazy + kShift) = 2^15.
+    constexpr float kShift = 7.0f;
 
     const int tid = threadIdx.x & (kThreads - 1), lane = tid & 63;
     // The wave index is the same on every lane; saying so lets every per-wave
@@ -394,7 +400,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     // log2-domain score per unit of int32 accumulator
     const float c = cq * ck * a.score_scale;
 
-    float m_run = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
+    float m_run = -INFINITY, m_sh = -INFINITY, l_run = 0.0f, s_run = 0.0f, inv_s = 0.0f;
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
@@ -450,7 +456,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             bool grow = mt > m_run + kLazy;
             if constexpr (KV_TOKEN) {
                 svt = sScale[buf][2 * kBN];
-                grow = grow || svt > s_run * 16.0f;
+                grow = grow || svt > s_run * 2.0f;
             }
             // Lazy rescale: the running max only moves when some row's max grows by
             // more than 2^kLazy (exp values stay <= 2^8, well inside fp16).
@@ -459,20 +465,27 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                 float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
                 float alpha_o = alpha;
                 if (KV_TOKEN) {
-                    // Values accumulate in units of s_run, the largest value scale so
-                    // far, so that p * v_scale / s_run stays bounded in fp16.
+                    // Values accumulate in units of s_run / 2^6, s_run the largest value
+                    // scale so far (within a factor 2), so that p * v_scale * 2^6 / s_run
+                    // stays below 2^15 in fp16 and above its subnormals where its weight
+                    // counts (the row sum is of p itself).
                     const float s_new = fmaxf(s_run, svt);
                     alpha_o = s_new > 0.0f ? alpha * (s_run / s_new) : alpha;
-                    inv_s = s_new > 0.0f ? 1.0f / s_new : 0.0f;
+                    inv_s = s_new > 0.0f ? 64.0f / s_new : 0.0f;
                     s_run = s_new;
                 }
                 m_run = m_new;
+                m_sh = KV_TOKEN ? m_new : m_new - kShift;
                 l_run *= alpha;
 #pragma unroll
                 for (int d = 0; d < DB; ++d) acc[d] *= alpha_o;
             }
 
             f16x8 phi[2][2], plo[2][2];
+            // The tile's weights are summed on their own and then added to the running
+            // sum once: small weights added one by one to a large running sum would
+            // each lose their low bits.
+            float l_tile = 0.0f;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -483,17 +496,17 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                         float p;
                         if (KV_TOKEN) {
                             // A row with nothing visible yet keeps m_run = -inf.
-                            p = __builtin_amdgcn_exp2f(x[16 * u + r] - m_run);
+                            p = __builtin_amdgcn_exp2f(x[16 * u + r] - m_sh);
                             if constexpr (need_mask) {
                                 if (x[16 * u + r] == -INFINITY) p = 0.0f;
                             }
                         } else {
-                            p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[u][r], c, -m_run));
+                            p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[u][r], c, -m_sh));
                             if constexpr (need_mask) {
                                 if (sc[u][r] == INT32_MIN) p = 0.0f;
                             }
                         }
-                        if (KV_TOKEN) l_run += p;
+                        if (KV_TOKEN) l_tile += p;
                         const float pv =
                             KV_TOKEN ? p * (sScale[buf][kBN + 32 * u + 16 * grp + r] * inv_s) : p;
                         const _Float16 hi16 = (_Float16)pv;
@@ -507,15 +520,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
 #pragma unroll
                         for (int e = 0; e < 8; e += 2) {
                             const f16x2 pr = {phi[u][s][e], phi[u][s][e + 1]};
-                            l_run = __builtin_amdgcn_fdot2(pr, one, l_run, false);
+                            l_tile = __builtin_amdgcn_fdot2(pr, one, l_tile, false);
                             if (PRECISE) {
                                 const f16x2 pl = {plo[u][s][e], plo[u][s][e + 1]};
-                                l_run = __builtin_amdgcn_fdot2(pl, one, l_run, false);
+                                l_tile = __builtin_amdgcn_fdot2(pl, one, l_tile, false);
                             }
                         }
                     }
                 }
             }
+            l_run += l_tile;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -616,8 +630,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
 #pragma unroll
         for (int d = 0; d < DB; ++d)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[d][i] *= s_run;
-        s_run = 1.0f;
+            for (int i = 0; i < 16; ++i) acc[d][i] *= s_run * (1.0f / 64.0f);
+        s_run = 64.0f;
     }
     if (MODE == kStream && sp.parts > 1) {
         // Leave this part in its slot (every lane: rows past q_len hold finite
@@ -719,7 +733,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
         l_tot = l;
     }
     if (!row_ok) return;
-    const float norm = (KV_TOKEN ? s_run : cv) / l_tot;
+    const float norm = (KV_TOKEN ? s_run * (1.0f / 64.0f) : cv) / l_tot;
     float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
@@ -733,11 +747,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     }
 }
 
-// Whether the values of (batch b, query head h)'s kv head reach above kPreciseAbove
+// Whether the values of (batch b, query head h)'s kv head reach above kHiOnlyMax
 // (per-tensor or per-head value scales): such items take P split into hi + lo.
 __device__ __forceinline__ bool item_is_wide(const PrefillArgs &a, int b, int h) {
     const int kvh = h / (a.q_heads / a.kv_heads);
-    return 127.0f * scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) > kPreciseAbove;
+    return 127.0f * scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) > kHiOnlyMax;
 }
 
 // Persistent form of the split kernel: one workgroup per compute unit takes the
@@ -1107,7 +1121,7 @@ extern "C" reef_status reef_attention_prefill_int8(
             }
             return launch_status();
         }
-        // Items whose values stay within kPreciseAbove take one fp16 P, the others the
+        // Items whose values stay within kHiOnlyMax take one fp16 P, the others the
         // hi + lo split (the precise kernel's grid); each launch skips the other's items.
         a.item_sel = 1;
         if (D == 128) REEF_STREAM_LAUNCH(128, false, false);
@@ -1135,7 +1149,7 @@ extern "C" reef_status reef_attention_prefill_int8(
             else REEF_SPLIT_LAUNCH(64, true);
             return launch_status();
         }
-        // Items whose values stay within kPreciseAbove take one fp16 P, the others the
+        // Items whose values stay within kHiOnlyMax take one fp16 P, the others the
         // hi + lo split; each launch skips the other's items.
         a.item_sel = 1;
         if (D == 128) REEF_SPLIT_LAUNCH(128, false);
@@ -1159,7 +1173,7 @@ extern "C" reef_status reef_attention_prefill_int8(
         }
         return launch_status();
     }
-    // Items whose values stay within kPreciseAbove take one fp16 P, the others the
+    // Items whose values stay within kHiOnlyMax take one fp16 P, the others the
     // hi + lo split; each launch returns at once from the other's items.
     a.item_sel = 1;
     if (D == 128) REEF_PREFILL_LAUNCH(128, false, false);

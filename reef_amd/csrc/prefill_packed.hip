@@ -20,15 +20,12 @@
 //     fp32 online softmax in base 2 with a lazy rescale, and O^T = V^T . P^T on
 //     v_mfma_f32_32x32x16_f16. The scores of tile j + 1 are issued before tile j's
 //     softmax so the matrix cores and the vector ALU work side by side.
-//   * Precision of P: for a value block whose dequantized magnitudes reach above
-//     kPreciseAbove, P is split into fp16 hi + lo parts (two products, 22 bits);
-//     below it, P is one fp16 (11 bits). Each P is then off by at most 2^-11 of
-//     itself, so an output by at most 2^-11 max|v_j - out|; when many keys share
-//     the weight the roundings mostly cancel (under 5.4e-4 on the benchmark
-//     workloads at |v| <= 6), but two dominant keys of values +-6 can move an
-//     output by 1.2e-3 (REEF_ATTN_PRECISE_PV splits every block). The
-//     activation-outlier channels of int8 LLM attention (|v| ~ 30) need the split.
-//     Each block keeps the row sum of exactly the P values its product uses.
+//   * Precision of P: when any 32-channel value block of a head has dequantized
+//     values above kHiOnlyMax (1), P is split into fp16 hi + lo parts (two products,
+//     22 bits) in every block; otherwise one fp16 P, each off by at most 2^-11 of
+//     itself, moves an output by at most 2^-11 max|v_j - out| < 1e-3. The
+//     probabilities carry an exponent offset (kShift) that keeps them out of the fp16
+//     subnormals, and the row sums are of exactly the P parts the products use.
 //   * Schedule: persistent workgroups; a causal head's query tiles t and T-1-t form
 //     one unit with the same number of key tiles as any other pair. Each XCD owns
 //     an eighth of the heads (a few at a time, whose K and V stay in that XCD's L2)
@@ -164,15 +161,18 @@ struct PackedArgs {
     uint32_t *queue;    // kQueueWords zero-filled words: next item per XCD, then done count
 };
 
-// Two probabilities (p0, p1) rounded to fp16 (the packed P operand) and the fp16
-// residuals p - fp16(p) of both (the lo operand). Each residual is exact in fp32
-// (fewer than 14 significant bits), one v_fma_mix_f32 reading the fp16 half.
+// Two probabilities rounded to fp16 (a packed P operand), and the fp16 of their
+// residuals p - fp16(p) (the lo operand). Each residual is exact in fp32 (one
+// v_fma_mix_f32 reading the fp16 half), so hi + lo carries 22 bits of p.
 __device__ __forceinline__ uint32_t pack_f16(float p0, float p1) {
     const f16x2 h = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){p0, p1},
                                             f16x2);
     return __builtin_bit_cast(uint32_t, h);
 }
 __device__ __forceinline__ uint32_t residual_f16(uint32_t hi, float p0, float p1) {
+    // Two fp32 residuals and one conversion: v_fma_mixlo/mixhi_f16 would take one
+    // instruction less but read their own destination, and beside matrix instructions
+    // they measured several times slower than this form.
     float r0, r1;
     asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r0) : "v"(hi), "v"(p0));
     asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
@@ -181,28 +181,9 @@ __device__ __forceinline__ uint32_t residual_f16(uint32_t hi, float p0, float p1
     return pack_f16(r0, r1);
 }
 
-__device__ __forceinline__ float scale_at(const float *s, int gran, int b, int h, int t, int heads,
-                                          int tokens) {
-    if (gran == REEF_SCALE_PER_TENSOR) return s[0];
-    if (gran == REEF_SCALE_PER_HEAD) return s[h];
-    return s[((int64_t)b * heads + h) * tokens + t];
-}
-
-// Scores accumulated from the float bias 1.5 * 2^23 (BIAS) read directly as floats:
-// the int32 sum 0x4B400000 + s is the bit pattern of 12582912 + s for |s| < 2^22
-// (|q.k| <= 128 * 128 * 128 = 2^21). The running max then lives in the same biased
-// log2 domain, m = (12582912 + s_max) c, and p = exp2((12582912 + s) c - m) is the
-// same probability up to one rounding of m, a factor common to a row that the row
-// sum cancels (rescales use differences of such m, exact by Sterbenz).
-constexpr int32_t kScoreBias = 0x4B400000;
-template <bool BIAS>
-__device__ __forceinline__ float score_float(int32_t x) {
-    return BIAS ? __int_as_float(x) : (float)x;
-}
-
-// Row sums on the matrix core: v_mfma_f32_16x16x32_f16 with A = a 0/1 pattern and
-// B = the 32 x 16 P operand, whose lane 16g + n holds row n (g = 0, 2) or row
-// 16 + n (g = 1, 3) of the score block. A row 0 sums the groups of rows 0-15, A
+// Row sums of the hi parts on the matrix core: v_mfma_f32_16x16x32_f16 with A = a 0/1
+// pattern and B = the 32 x 16 P operand, whose lane 16g + n holds row n (g = 0, 2) or
+// row 16 + n (g = 1, 3) of the score block. A row 0 sums the groups of rows 0-15, A
 // row 1 those of rows 16-31: lane n (< 16) accumulates row n in register 0 and row
 // 16 + n in register 1 (the other lanes' registers stay zero).
 __device__ __forceinline__ f16x8 row_sum_pattern(int lane) {
@@ -224,15 +205,57 @@ __device__ __forceinline__ void scale_row_sums(f32x4 &rs, float alpha, int lane)
     rs[1] *= upper;
 }
 
-// One query tile (128 rows) of one (batch, head), one wave per 32 rows. LO: some
-// value block splits P into hi + lo (pmask bit d: channels 32d .. 32d + 31). BIAS:
-// see kScoreBias. Per key tile j the wave issues the scores of tile j + 1 on the
-// matrix cores first and then runs tile j's softmax on the vector ALU, so the two
-// overlap; tile j's P.V follows. Not inlined: each variant's loop has the whole
-// scalar register file (inlined into the item loop, the variants' scalars spilled).
-// Arguments of a called function arrive in vector registers; the tile function
-// moves every launch-wide value back to scalar registers so that buffer
-// descriptors and LDS destinations stay scalar (no per-lane loops).
+__device__ __forceinline__ float scale_at(const float *s, int gran, int b, int h, int t, int heads,
+                                          int tokens) {
+    if (gran == REEF_SCALE_PER_TENSOR) return s[0];
+    if (gran == REEF_SCALE_PER_HEAD) return s[h];
+    return s[((int64_t)b * heads + h) * tokens + t];
+}
+
+// Scores relative to the row's running maximum s_run, read as floats without a
+// conversion: the integer product accumulates from the bit pattern 0x4B400000 - s_run,
+// so the int32 result is the bit pattern of the float 12582912 + (s - s_run) for
+// |s - s_run| <= 2^22 (|q.k| <= 128 * 128 * 128 = 2^21). The probability
+// p = exp2((s - s_run) c + kShift) is then one FMA and an exp2: exp2(sf c - kc) with
+// the per-row constant kc = 12582912 c - kShift, whose single rounding (within 1/4
+// when c <= 1/2) is a factor common to the row that the row sum cancels. With a
+// larger c the exact difference sf - 12582912 comes first (FAST = false).
+//
+// The running maximum moves when a row's largest score exceeds it by more than kLazy
+// (log2 units). Then every p lies below 2^(kLazy + kShift + 1/4) < 2^16, inside the
+// fp16 range, and the row's leading key has p >= 2^(kShift - 1/4): a key of weight
+// 2^-22 of it still has a normal fp16 p (hi and lo keep 11 bits each), and below
+// that every p is off by at most 2^-25, under 2^-33 of the row sum per key.
+constexpr int32_t kScoreBias = 0x4B400000;
+constexpr float kBiasF = 12582912.0f;
+constexpr float kLazy = 6.0f;
+constexpr float kShift = 9.0f;
+constexpr float kFastCMax = 0.5f;
+constexpr int32_t kMasked = 0;  // below every biased score (>= 0x4B000000)
+
+__device__ __forceinline__ int32_t imax3(int32_t a, int32_t b, int32_t c) {
+    return max(max(a, b), c);
+}
+
+// One query tile (128 rows) of one (batch, head), one wave per 32 rows. LO: P is
+// hi + lo in every value block. FAST: see kScoreBias.
+//
+// Per 64-key tile j a wave issues 40 matrix instructions: the 8 score products of
+// tile j + 1 (K rows permuted so that each lane's scores are the P operand of the
+// value products), then for each of the four 16-key chunks of tile j its 4 hi and 4
+// lo value products (one per 32-channel block). The vector work of tile j (exp2 of
+// the scores, fp16 hi and lo, the row sum) runs one chunk ahead of the products
+// that use it, between the matrix instructions: chunk 0 beside the score products,
+// chunk c + 1 beside chunk c's products, and the row maximum of tile j + 1 beside
+// chunk 3's. Scheduling barriers pin that interleave, so that the matrix core and
+// the vector ALU of a SIMD work side by side within one wave as well as across the
+// two waves of the SIMD.
+//
+// Not inlined: each variant's loop has the whole scalar register file (inlined
+// into the item loop, the variants' scalars spilled). Arguments of a called
+// function arrive in vector registers; the tile function moves every launch-wide
+// value back to scalar registers so that buffer descriptors and LDS destinations
+// stay scalar (no per-lane loops).
 __device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 __device__ __forceinline__ float uni(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int32_t, x)));
@@ -264,17 +287,28 @@ __device__ __forceinline__ PackedArgs uniform_args(const PackedArgs &x) {
     return a;
 }
 
-template <bool LO, bool BIAS>
+#define REEF_SLOT() __builtin_amdgcn_sched_barrier(0)
+// Empty asm statements that hold a vector value in place: pin() makes the value
+// appear at this point (work that reads it cannot move above), keep() makes it
+// needed at this point (work that computes it cannot move below). Together with the
+// scheduling barriers they keep each slot's vector work in its slot. Only values of
+// vector instructions (or long-finished matrix results) pass through them.
+template <class T>
+__device__ __forceinline__ void pin(T &x) {
+    asm volatile("" : "+v"(x));
+}
+template <class T>
+__device__ __forceinline__ void keep(const T &x) {
+    asm volatile("" ::"v"(x));
+}
+
+template <bool LO, bool FAST>
 __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, int b_in, int h_in,
-                                                      int tile_in, int8_t *smem_in,
-                                                      uint32_t pmask_in) {
+                                                      int tile_in, int8_t *smem_in) {
     const PackedArgs a = uniform_args(args);
     const int b = uni(b_in), h = uni(h_in), tile = uni(tile_in);
     int8_t *const smem = uni(smem_in);
-    const uint32_t pmask = (uint32_t)uni((int32_t)pmask_in);
     constexpr int DB = kPD / 32;
-    constexpr float kLazy = 8.0f;  // the running max moves when a row max grows by > 2^8
-    constexpr int32_t kMasked = BIAS ? 0 : INT32_MIN;  // below every score
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, grp = lane >> 5;
@@ -309,6 +343,9 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
     const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float c = cq * ck * a.score_scale;  // log2-domain score per unit of int32 sum
+    const float kc = __builtin_fmaf(kBiasF, c, -kShift);
+    // Largest integer growth of a row maximum that stays within kLazy.
+    const int32_t lazy_i = (int32_t)fminf(kLazy / c, 8388608.0f);
 
     // Direct loads: wave w fills 1 KB blocks w, w + 4, ... of a K tile and of a V
     // tile. Lane L of K block kb writes LDS row 8 kb + L / 8 at position L % 8,
@@ -349,20 +386,24 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
 
     // LDS operand positions: K row 32u + col, chunk 2t + grp; V row 32d + col, chunk
     // 4u + 2 grp + s (keys 32u + 16 grp + 8s .. + 8, the P operand's keys).
-    int kpos[kPD / 32], vpos[2][2];
+    int kpos[kPD / 32], vpos[4];
 #pragma unroll
     for (int t = 0; t < kPD / 32; ++t) kpos[t] = col * kPD + 16 * swz(col, 2 * t + grp);
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) vpos[u][s] = col * 128 + 16 * swz(col, 4 * u + 2 * grp + s);
-    const f16x8 ones = row_sum_pattern(lane);
-    const i32x16 bias = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
-                         kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
-                         kScoreBias, kScoreBias, kScoreBias, kScoreBias};
+    for (int cc = 0; cc < 4; ++cc)
+        vpos[cc] = col * 128 + 16 * swz(col, 4 * (cc >> 1) + 2 * grp + (cc & 1));
 
-    float m_run = -INFINITY;
-    f32x4 rs_hi = {}, rs_lo = {};
+    int32_t s_run = -(1 << 21);  // the row's running maximum of integer scores
+    i32x16 bias;                 // kScoreBias - s_run in every element
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bias[r] = kScoreBias - s_run;
+    // Row sums of exactly the P parts the products use: the hi parts on the matrix core
+    // (rs), the lo parts in packed fp16 per tile (lsum; a tile's lo parts sum below
+    // 2^10, so its rounding is under 2^-11 of a term that is itself 2^-11 of the row
+    // sum) added into this lane's fp32 share (l_lo).
+    const f16x8 ones = row_sum_pattern(lane);
+    f32x4 rs = {};
+    float l_lo = 0.0f;
     f32x16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
@@ -371,102 +412,111 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     };
 
     struct Scores {
-        i32x16 u[2];
+        i32x16 u[2];  // keys 32u .. 32u + 31 of a tile: register r of lane group g is key 16g + r
     };
-    auto scores = [&](int j) {  // scores of tile j, keys 32u .. 32u + 31 in u[u]
-        const int8_t *sK = kring + (j % kSlots) * kKTile;
-        Scores out;
-        i32x4 kop[2][kPD / 32];
+    // The lane's largest score of a tile, then the row's (both lane groups).
+    auto lane_max = [](const Scores &sc) {
+        int32_t t[11];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int t = 0; t < kPD / 32; ++t)
-                kop[u][t] = *reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]);
-        
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int t = 0; t < kPD / 32; ++t)
-                out.u[u] = mfma_32x32x32_i8(kop[u][t], qop[t],
-                                            t == 0 ? (BIAS ? bias : i32x16{}) : out.u[u]);
-        return out;
+        for (int i = 0; i < 10; ++i) {
+            const int k0 = 3 * i, k1 = 3 * i + 1, k2 = 3 * i + 2;
+            t[i] = imax3(sc.u[k0 >> 4][k0 & 15], sc.u[k1 >> 4][k1 & 15], sc.u[k2 >> 4][k2 & 15]);
+        }
+        t[10] = max(sc.u[1][14], sc.u[1][15]);
+        const int32_t a0 = imax3(t[0], t[1], t[2]), a1 = imax3(t[3], t[4], t[5]);
+        const int32_t a2 = imax3(t[6], t[7], t[8]), a3 = max(t[9], t[10]);
+        return max(imax3(a0, a1, a2), a3);
     };
-    // Tile j: masks, the lazy rescale, the probabilities and their row sums, P.V.
-    auto tile_math = [&](const int j, auto masked_tag, Scores sc, auto &&after_rescale) {
-        constexpr bool MASKED = decltype(masked_tag)::value;
+    auto row_max = [](int32_t m) {
+        const auto r = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+        return max((int32_t)r[0], (int32_t)r[1]);
+    };
+    auto mask_scores = [&](Scores &sc, int j) {  // keys outside [lo, hi] of tile j
         const int kt = kt0 + kPK * j;
-        bool need = false;
-        if constexpr (MASKED) {
-            need = !(kt + kPK - 1 <= full_hi && kt >= full_lo);  // uniform
-            if (need) {
+        if (!(kt + kPK - 1 <= full_hi && kt >= full_lo)) {  // uniform
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = kt + 32 * u + 16 * grp + r;
-                        if (key < lo || key > hi) sc.u[u][r] = kMasked;
-                    }
-            }
-        }
-        int mi = sc.u[0][0];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int r = (u == 0 ? 1 : 0); r < 16; ++r) mi = max(mi, sc.u[u][r]);
-        // c > 0, so the largest float score is c times the largest integer.
-        float mt = mi == kMasked ? -INFINITY : score_float<BIAS>(mi) * c;
-        mt = xor32_max(mt);
-        if (__any(mt > m_run + kLazy)) {  // wave-uniform
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            scale_row_sums(rs_hi, alpha, lane);
-            if (LO) scale_row_sums(rs_lo, alpha, lane);
-#pragma unroll
-            for (int d = 0; d < DB; ++d) acc[d] *= alpha;
-        }
-        after_rescale();
-        // Per chunk of 16 keys: the probabilities, their fp16 row sums, then the
-        // products (the residual products of the value blocks that need them right
-        // after, so that a chunk's residuals die with it).
-        const int8_t *sV = vring + (j % kSlots) * kVTile;
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                uint32_t phi[4], plo[4];
-                f16x8 vop[DB];
-#pragma unroll
-                for (int d = 0; d < DB; ++d)
-                    vop[d] = *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[u][s]);
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    float p[2];
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const int r = 8 * s + e + i;
-                        p[i] = __builtin_amdgcn_exp2f(
-                            __builtin_fmaf(score_float<BIAS>(sc.u[u][r]), c, -m_run));
-                        // a masked key of a row with nothing visible yet (m_run = -inf)
-                        if (MASKED && need && sc.u[u][r] == kMasked) p[i] = 0.0f;
-                    }
-                    const uint32_t hw = pack_f16(p[0], p[1]);
-                    phi[e / 2] = hw;
-                    if (LO) plo[e / 2] = residual_f16(hw, p[0], p[1]);
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kt + 32 * u + 16 * grp + r;
+                    if (key < lo || key > hi) sc.u[u][r] = kMasked;
                 }
-                rs_hi = mfma_16x16x32_f16(ones, operand(phi), rs_hi);
-                if (LO) rs_lo = mfma_16x16x32_f16(ones, operand(plo), rs_lo);
-                __builtin_amdgcn_s_setprio(1);
+            return true;
+        }
+        return false;
+    };
+    // The lazy rescale before tile j's probabilities, from this lane's maximum mx of
+    // the tile: when some score exceeds s_run by more than lazy_i, each row moves s_run
+    // to its maximum, and the scores already computed against the old s_run move with
+    // it.
+    auto rescale = [&](Scores &sc, int32_t mx) {
+        if (__any(mx - kScoreBias > lazy_i)) {  // wave-uniform
+            // The row's maximum over both lane groups (a cross-lane swap, which waits
+            // for the matrix instructions in flight: only here, on the rare rescale).
+            const int32_t d = row_max(mx) - kScoreBias;
+            const int32_t delta = d > 0 ? d : 0;
+            s_run += delta;
+            const float alpha = __builtin_amdgcn_exp2f(-(float)delta * c);
+            scale_row_sums(rs, alpha, lane);
+            l_lo *= alpha;
 #pragma unroll
-                for (int d = 0; d < DB; ++d) acc[d] = mfma_32x32x16_f16(vop[d], operand(phi), acc[d]);
-                if (LO) {
+            for (int dd = 0; dd < DB; ++dd) acc[dd] *= alpha;
 #pragma unroll
-                    for (int d = 0; d < DB; ++d)
-                        if ((pmask >> d) & 1)  // uniform
-                            acc[d] = mfma_32x32x16_f16(vop[d], operand(plo), acc[d]);
-                }
-                __builtin_amdgcn_s_setprio(0);
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sc.u[u][r] -= delta;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bias[r] = kScoreBias - s_run;
+        }
+    };
+    // Keys 8s + e .. 8s + e + 3 of chunk cc = 2u + s in two stages, placed a matrix
+    // instruction apart so that the exp2 latency is covered: expo() the probabilities
+    // p in fp32, pack() their fp16 hi and lo parts and the lo parts' sum. A masked key
+    // (or, after a rescale, a masked key moved below zero) has p = 0.
+    auto expo = [&](const Scores &sc, int cc, int e, float (&p)[4], auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        int32_t x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[i] = sc.u[cc >> 1][8 * (cc & 1) + e + i];
+            pin(x[i]);
+        }
+        float arg[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float sf = __int_as_float(x[i]);
+            arg[i] = FAST ? __builtin_fmaf(sf, c, -kc) : __builtin_fmaf(sf - kBiasF, c, kShift);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(arg[i]);
+            if (MASKED) p[i] = x[i] <= kMasked ? 0.0f : p[i];
+            keep(p[i]);
+        }
+    };
+    auto pack = [&](int e, const float (&p)[4], uint32_t (&ph)[4], uint32_t (&pl)[4],
+                    f16x2 &lsum) {
+        float q[4] = {p[0], p[1], p[2], p[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pin(q[i]);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t hw = pack_f16(q[2 * k], q[2 * k + 1]);
+            ph[e / 2 + k] = hw;
+            keep(hw);
+        }
+        if (LO) {
+            uint32_t lw[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) lw[k] = residual_f16(ph[e / 2 + k], q[2 * k], q[2 * k + 1]);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                pl[e / 2 + k] = lw[k];
+                keep(lw[k]);
             }
+            lsum += __builtin_bit_cast(f16x2, lw[0]) + __builtin_bit_cast(f16x2, lw[1]);
+            keep(lsum);
+        }
     };
 
     // Loads: K of tile 0, then per iteration g the group {K(g + 1), V(g)}, issued two
@@ -491,62 +541,171 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         }
     };
     static_assert(kKBlocks + kVBlocks < 16, "vmcnt fits the low field");
+
+    struct Tile {
+        Scores s;
+        int32_t mx;  // this lane's maximum of s
+    };
+    // Scores of tile 0 (the prologue; later tiles' scores come from step()).
+    auto first_scores = [&]() {
+        Tile t;
+        const int8_t *sK = kring;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tt = 0; tt < kPD / 32; ++tt) {
+                const i32x4 kop = *reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[tt]);
+                t.s.u[u] = mfma_32x32x32_i8(kop, qop[tt], tt == 0 ? bias : t.s.u[u]);
+            }
+        mask_scores(t.s, 0);
+        t.mx = lane_max(t.s);
+        return t;
+    };
+
+    // Tile j: wait for its loads, rescale, then the interleaved products and vector
+    // work described above; returns tile j + 1's scores and row maximum. Past the last
+    // tile the scores are computed from a stale K slot (no slot is being written at
+    // that point) and discarded.
+    auto step = [&](const int j, auto masked_tag, auto mask_next_tag, Tile &cur) {
+        constexpr bool MASK_NEXT = decltype(mask_next_tag)::value;
+        wait_loads(group_loads(j + 1));
+        __builtin_amdgcn_s_barrier();
+        issue_group(j + 2);
+        rescale(cur.s, cur.mx);
+        const int8_t *sK = kring + ((j + 1) % kSlots) * kKTile;
+        const int8_t *sV = vring + (j % kSlots) * kVTile;
+        i32x4 kop[2][kPD / 32];
+        f16x8 vop[4][DB];
+        uint32_t ph[4][4], pl[4][4];
+        Tile nx;
+        auto kread = [&](int u, int t) {
+            kop[u][t] = *reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]);
+        };
+        auto vread = [&](int cc) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                vop[cc][d] = *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[cc]);
+        };
+        auto qk = [&](int u, int t) {
+            nx.s.u[u] = mfma_32x32x32_i8(kop[u][t], qop[t], t == 0 ? bias : nx.s.u[u]);
+        };
+        auto pv = [&](int cc, int d, bool lo_part) {
+            acc[d] = mfma_32x32x16_f16(vop[cc][d], operand(lo_part ? pl[cc] : ph[cc]), acc[d]);
+        };
+        f16x2 lsum = {};
+        float pe[4][2][4];  // fp32 p of chunk cc, keys 4h .. 4h + 3, between the two stages
+        auto ex = [&](int cc, int hh) { expo(cur.s, cc, 4 * hh, pe[cc][hh], masked_tag); };
+        auto pk = [&](int cc, int hh) { pack(4 * hh, pe[cc][hh], ph[cc], pl[cc], lsum); };
+        // This tile's hi row sums on their own, added to the running sums once per tile.
+        f32x4 rs_tile = {};
+        auto rsum = [&](int cc) { rs_tile = mfma_16x16x32_f16(ones, operand(ph[cc]), rs_tile); };
+
+        kread(0, 0);
+        kread(1, 0);
+        kread(0, 1);
+        kread(1, 1);
+        vread(0);
+        REEF_SLOT();
+        // Score products of tile j + 1 beside chunk 0's probabilities and chunk 1's
+        // exponentials.
+        ex(0, 0);
+        qk(0, 0);
+        REEF_SLOT();
+        ex(0, 1);
+        qk(1, 0);
+        REEF_SLOT();
+        kread(0, 2);
+        kread(1, 2);
+        kread(0, 3);
+        kread(1, 3);
+        pk(0, 0);
+        qk(0, 1);
+        REEF_SLOT();
+        pk(0, 1);
+        qk(1, 1);
+        REEF_SLOT();
+        ex(1, 0);
+        qk(0, 2);
+        REEF_SLOT();
+        ex(1, 1);
+        qk(1, 2);
+        REEF_SLOT();
+        qk(0, 3);
+        REEF_SLOT();
+        qk(1, 3);
+        REEF_SLOT();
+        // Chunk cc's row sum and value products beside chunk cc + 1's packing and chunk
+        // cc + 2's exponentials (for the last chunks, beside tile j + 1's row maximum).
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            if (cc < 3) vread(cc + 1);
+            rsum(cc);
+            REEF_SLOT();
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                if (cc < 3 && d < 2) pk(cc + 1, d);
+                if (cc < 2 && d >= 2) ex(cc + 2, d - 2);
+                if (cc == 2 && d == 2) {
+                    pin(nx.s.u[0]);
+                    pin(nx.s.u[1]);
+                    nx.mx = lane_max(nx.s);
+                    keep(nx.mx);
+                }
+                pv(cc, d, false);
+                REEF_SLOT();
+            }
+            if (LO) {
+#pragma unroll
+                for (int d = 0; d < DB; ++d) {
+                    pv(cc, d, true);
+                    REEF_SLOT();
+                }
+            }
+        }
+        if (LO) l_lo += (float)lsum[0] + (float)lsum[1];
+        rs[0] += rs_tile[0];
+        rs[1] += rs_tile[1];
+        if (MASK_NEXT && mask_scores(nx.s, j + 1)) nx.mx = lane_max(nx.s);
+        return nx;
+    };
+
     issue_k(0);
     issue_group(0);
     issue_group(1);
     wait_loads(group_loads(0) + group_loads(1));
     __builtin_amdgcn_s_barrier();
-    Scores sc = scores(0);
+    Tile tl = first_scores();
     // Tiles [it_a, it_b) are whole for every row of the workgroup: no masks.
     const int wg_full_lo = a.window > 0 ? a.query_start + r_last + 1 - a.window : 0;
     const int wg_full_hi = min(a.query_start + q0, a.kv_len - 1);
     const int it_a = max(0, wg_full_lo - kt0 + kPK - 1) / kPK;
     const int span = wg_full_hi + 1 - kt0;
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kPK : 0));
-    // Tile j's softmax and products, with the scores of tile j + 1 issued between the
-    // rescale and the probabilities, in the same straight-line code as tile j's
-    // products, so that the matrix and vector instructions interleave; returns those
-    // scores. Past the last tile they are computed from a stale K slot (no slot is
-    // being written at that point) and discarded.
-    auto step = [&](const int j, auto masked_tag, const Scores &cur) {
-        wait_loads(group_loads(j + 1));
-        __builtin_amdgcn_s_barrier();
-        issue_group(j + 2);
-        Scores next;
-        // The wave raises its issue priority while it issues matrix instructions, so
-        // that of the two waves on a SIMD the one with products to issue goes first
-        // and the other fills in with its vector work (2.4 % on 4x32x8192x128).
-        tile_math(j, masked_tag, cur, [&] {
-            __builtin_amdgcn_s_setprio(1);
-            next = scores(j + 1);
-            __builtin_amdgcn_s_setprio(0);
-        });
-        return next;
-    };
     // Two tiles per iteration: the loop-carried scores come back in the registers
     // they left, with no copies.
+    // Tile j + 1 needs its scores masked only when it lies outside [it_a, it_b).
     int j = 0;
-    auto run = [&](const int end, auto masked_tag) {
+    auto run = [&](const int end, auto masked_tag, auto mask_next_tag) {
         for (; j + 1 < end; j += 2) {
-            const Scores mid = step(j, masked_tag, sc);
-            sc = step(j + 1, masked_tag, mid);
+            Tile mid = step(j, masked_tag, mask_next_tag, tl);
+            tl = step(j + 1, masked_tag, mask_next_tag, mid);
         }
         if (j < end) {
-            sc = step(j, masked_tag, sc);
+            tl = step(j, masked_tag, mask_next_tag, tl);
             ++j;
         }
     };
-    run(it_a, std::true_type{});
-    run(it_b, std::false_type{});
-    run(n_tiles, std::true_type{});
+    run(it_a, std::true_type{}, std::true_type{});
+    run(it_b - 1, std::false_type{}, std::false_type{});
+    run(it_b, std::false_type{}, std::true_type{});
+    run(n_tiles, std::true_type{}, std::true_type{});
 
-    const float lh = row_sum_of_lane(rs_hi, lane);
-    const float ll = LO ? row_sum_of_lane(rs_lo, lane) : 0.0f;
+    const float l_row = row_sum_of_lane(rs, lane) + (LO ? xor32_sum(l_lo) : 0.0f);
     if (row_ok) {
         float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
+        const float norm = cv / l_row;
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
-            const float norm = cv / (LO && ((pmask >> d) & 1) ? lh + ll : lh);
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
                 f32x4 o;
@@ -560,38 +719,27 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     __syncthreads();
 }
 
-// Blocks of (batch, kv head) whose dequantized values reach above kPreciseAbove:
-// the largest |code| of each 32-channel block over the head's tiles, times the
-// value scale. Uniform over the workgroup.
-__device__ __forceinline__ uint32_t precise_blocks(const PackedArgs &a, int b, int kvh,
-                                                   uint32_t *sRed) {
-    if (a.all_precise) return 0xFu;
+// Whether P needs hi + lo parts for (batch, kv head): some dequantized value of the
+// head reaches above kHiOnlyMax (the largest |code| of each 32-channel block over
+// the head's tiles, times the value scale). Uniform over the workgroup.
+__device__ __forceinline__ bool needs_lo(const PackedArgs &a, int b, int kvh, uint32_t *sRed) {
+    if (a.all_precise) return true;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t *bm = a.bmax + (int64_t)(b * a.kv_heads + kvh) * a.kv_tiles;
-    uint32_t m[4] = {0, 0, 0, 0};
+    uint32_t m = 0;
     for (int t = tid; t < a.kv_tiles; t += 64 * kWaves) {
         const uint32_t w = bm[t];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) m[i] = max(m[i], (w >> (8 * i)) & 0xffu);
+        for (int i = 0; i < 4; ++i) m = max(m, (w >> (8 * i)) & 0xffu);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m[i] = wave_max_u32(m[i]);
-    if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sRed[wave * 4 + i] = m[i];
-    }
+    m = wave_max_u32(m);
+    if (lane == 0) sRed[wave] = m;
     __syncthreads();
-    uint32_t top[4] = {0, 0, 0, 0};
-    for (int w = 0; w < kWaves; ++w)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) top[i] = max(top[i], sRed[w * 4 + i]);
+    uint32_t top = 0;
+    for (int w = 0; w < kWaves; ++w) top = max(top, sRed[w]);
     __syncthreads();  // sRed is reused by the next item
     const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-    uint32_t mask = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if ((float)top[i] * cv > kPreciseAbove) mask |= 1u << i;
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)mask);
+    return __builtin_amdgcn_readfirstlane((int)((float)top * cv > kHiOnlyMax)) != 0;
 }
 
 // XCD y's share of the work: the (batch, head) pairs [bh0, bh0 + nh), an eighth of
@@ -663,25 +811,26 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(Pac
         }
         const int b = bh / a.q_heads, h = bh % a.q_heads;
         const int kvh = h / (a.q_heads / a.kv_heads);
-        const uint32_t pmask = precise_blocks(a, b, kvh, sRed);
-        // Scores read as biased floats need the biased maximum's rounding (half an
-        // ulp of 12582912 c) well below the lazy-rescale margin: c <= 4 (any q
-        // scale granularity but per token, where c varies by row).
-        const bool biased =
-            a.q_gran != REEF_SCALE_PER_TOKEN &&
-            scale_at(a.qs, a.q_gran, b, h, 0, a.q_heads, a.q_len) *
-                    scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) * a.score_scale <=
-                4.0f;
-        auto run = [&](auto lo_tag, auto bias_tag) {
-            constexpr bool LO = decltype(lo_tag)::value, BIAS = decltype(bias_tag)::value;
-            packed_tile<LO, BIAS>(a, b, h, first, smem, pmask);
-            if (second >= 0) packed_tile<LO, BIAS>(a, b, h, second, smem, pmask);
+        const bool lo = needs_lo(a, b, kvh, sRed);
+        // One FMA per probability when the score factor c is small enough that
+        // 12582912 c rounds within 1/4 (any q scale granularity but per token, where c
+        // varies by row).
+        const float c_item = a.q_gran == REEF_SCALE_PER_TOKEN
+                                 ? INFINITY
+                                 : scale_at(a.qs, a.q_gran, b, h, 0, a.q_heads, a.q_len) *
+                                       scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) *
+                                       a.score_scale;
+        const bool fast = c_item <= kFastCMax;
+        auto run = [&](auto lo_tag, auto fast_tag) {
+            constexpr bool LO = decltype(lo_tag)::value, FAST = decltype(fast_tag)::value;
+            packed_tile<LO, FAST>(a, b, h, first, smem);
+            if (second >= 0) packed_tile<LO, FAST>(a, b, h, second, smem);
         };
-        if (pmask) {
-            if (biased) run(std::true_type{}, std::true_type{});
+        if (lo) {
+            if (fast) run(std::true_type{}, std::true_type{});
             else run(std::true_type{}, std::false_type{});
         } else {
-            if (biased) run(std::false_type{}, std::true_type{});
+            if (fast) run(std::false_type{}, std::true_type{});
             else run(std::false_type{}, std::false_type{});
         }
     }

@@ -114,6 +114,53 @@ def test_prefill_workload_full_size(reef, name):
     print(f"{name}: max_abs_err {worst:.3e}", flush=True)
 
 
+def _fp64_attention_rows(q, k, v, qs, ks, vs, b, h, kvh, scale, gran, r0, r1):
+    """Rows r0 .. r1 - 1 of causal attention for (batch b, q head h) in float64 on the
+    GPU over the dequantized int8 inputs: float(q) s_q . float(k) s_k * scale, softmax,
+    times float(v) s_v. A second opinion beside the oracle's sampled rows, fast enough
+    to cover every row of a workload."""
+    sq = qs[h] if gran == 1 else qs[0]
+    sk = ks[kvh] if gran == 1 else ks[0]
+    sv = vs[kvh] if gran == 1 else vs[0]
+    qf = q[b, h, r0:r1].to(torch.float64) * sq.to(torch.float64)
+    kf = k[b, kvh, :r1].to(torch.float64).contiguous() * sk.to(torch.float64)
+    vf = v[b, kvh, :r1].to(torch.float64).contiguous() * sv.to(torch.float64)
+    s = torch.matmul(qf, kf.t().contiguous()) * scale
+    rows = torch.arange(r0, r1, device=s.device)[:, None]
+    keys = torch.arange(r1, device=s.device)[None, :]
+    s = s.masked_fill(keys > rows, float("-inf"))
+    pr = torch.softmax(s, dim=1)
+    return torch.matmul(pr, vf)
+
+
+@pytest.mark.parametrize("name", ["prefill_1x32x2048x128", "prefill_1x8x4096x128_gqa",
+                                  "prefill_4x32x8192x128"])
+def test_prefill_workload_every_row(reef, name):
+    """Every output row of the benchmark workload from the bench's launch (the library's
+    default precision) against float64 attention on the GPU, within TOL."""
+    cfg = W.CONFIGS[name]
+    case(f"{cfg.name}: bench launch, every row vs float64 attention")
+    cfg, fp32_inputs, (q, k, v, qs, ks, vs), out, launch = bench.prefill_setup(torch, reef, W,
+                                                                              name)
+    del fp32_inputs
+    launch()
+    torch.cuda.synchronize()
+    S = cfg.seq
+    group = cfg.q_heads // cfg.kv_heads
+    chunk = 2048
+    worst = 0.0
+    for b in range(cfg.batch):
+        for h in range(cfg.q_heads):
+            for r0 in range(0, S, chunk):
+                r1 = min(S, r0 + chunk)
+                ref = _fp64_attention_rows(q, k, v, qs, ks, vs, b, h, h // group,
+                                           cfg.softmax_scale, cfg.granularity, r0, r1)
+                err = float((out[b, h, r0:r1].to(torch.float64) - ref).abs().max())
+                worst = max(worst, err)
+                assert err <= TOL, (b, h, r0, err)
+    print(f"{name}: every row, max_abs_err {worst:.3e}", flush=True)
+
+
 def _decode_gold(qq, qs, k_tok, v_tok, ks, vs, L, scale):
     """One sequence: qq [Hq, D] int8 with per-head scales qs [Hq]; k_tok, v_tok
     [Hkv, >= L, D] int8; ks, vs [Hkv, >= L] per-token scales."""
