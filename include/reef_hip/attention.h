@@ -223,6 +223,23 @@ reef_status reef_qk_scores_i32(const int8_t *q, const int8_t *k, int64_t batch, 
                                int64_t kv_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,
                                int32_t *acc, hipStream_t stream);
 
+/* The same scores from the packed schedule's own kernel (head_dim 128; the
+ * matmul<int8_t, int32_t> of tensor.hpp:210-246 on q . k^T): it runs one attention
+ * over (q, k, v = k) in which every row sees every key, and stores every score
+ * accumulator as its tile code reads it (keys staged in LDS in its permuted order,
+ * accumulators relative to the running maximum), turned back into the plain int32
+ * sum. acc: [B, Hq, q_len, kv_len] int32; packed q [B, Hq, q_len, 128] and k
+ * [B, Hkv, kv_len, 128]; workspace: 256-byte aligned, zero-filled once (the launch
+ * leaves it zero-filled where it must be), at least
+ * reef_qk_scores_i32_packed_workspace_bytes() bytes (0: invalid sizes). A test hook. */
+size_t reef_qk_scores_i32_packed_workspace_bytes(int64_t batch, int64_t q_heads,
+                                                 int64_t kv_heads, int64_t q_len,
+                                                 int64_t kv_len);
+reef_status reef_qk_scores_i32_packed(const int8_t *q, const int8_t *k, int64_t batch,
+                                      int64_t q_heads, int64_t kv_heads, int64_t q_len,
+                                      int64_t kv_len, int32_t *acc, void *workspace,
+                                      size_t workspace_bytes, hipStream_t stream);
+
 /* Integer-only attention: attend_head_int8 (int8.hpp:250-279) for every (batch,
  * head) in one launch, bit-identical to the engine. Per row: int32 scores over the
  * visible keys, weights table[min((max - s) >> score_shift, 255)], probabilities

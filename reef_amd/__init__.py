@@ -33,6 +33,7 @@ EXPORTS = [
     "reef_quantize_int8_per_tensor", "reef_quantize_int8_per_head",
     "reef_quantize_int8_per_token", "reef_dequantize_int8", "reef_read_status_word",
     "reef_attention_prefill_workspace_bytes", "reef_attention_prefill_int8", "reef_qk_scores_i32",
+    "reef_qk_scores_i32_packed_workspace_bytes", "reef_qk_scores_i32_packed",
     "reef_attention_decode_workspace_bytes", "reef_attention_decode_int8",
     "reef_attention_decode_int8_paged", "reef_attention_decode_int8_paged_noalloc",
     "reef_kv_pack_v_pages", "reef_kv_append_int8",
@@ -113,6 +114,8 @@ _SIGS = {
                                     C.POINTER(Strides), _P, C.POINTER(Strides), _P, _P, _P, _P,
                                     C.POINTER(Strides), _P, C.c_size_t, _P],
     "reef_qk_scores_i32": [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "reef_qk_scores_i32_packed_workspace_bytes": [_I64, _I64, _I64, _I64, _I64],
+    "reef_qk_scores_i32_packed": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, C.c_size_t, _P],
     "reef_attention_decode_workspace_bytes": [C.POINTER(DecodeParams)],
     "reef_attention_decode_int8": [C.POINTER(DecodeParams), _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    C.c_size_t, _P, _P],
@@ -391,6 +394,28 @@ def qk_scores_i32(q, k):
     acc = torch.empty((B, Hq, Sq, Skv), dtype=torch.int32, device=q.device)
     check(lib().reef_qk_scores_i32(_ptr(q), _ptr(k), B, Hq, Hkv, Sq, Skv, D, _ptr(acc),
                                    _stream()), "qk_scores_i32")
+    return acc
+
+
+def qk_scores_i32_packed(q, k):
+    """int32 q . k^T for packed q [B, Hq, Sq, 128] and k [B, Hkv, Skv, 128], read from
+    the packed prefill kernel's own score accumulators."""
+    torch = _torch()
+    _require(q, torch.int8, "q")
+    _require(k, torch.int8, "k")
+    q = q.contiguous()
+    k = k.contiguous()
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    if D != 128:
+        raise ValueError("the packed score hook takes head_dim 128")
+    acc = torch.full((B, Hq, Sq, Skv), -1, dtype=torch.int32, device=q.device)
+    nbytes = lib().reef_qk_scores_i32_packed_workspace_bytes(B, Hq, Hkv, Sq, Skv)
+    if nbytes == 0:
+        raise ValueError("qk_scores_i32_packed: invalid sizes")
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=q.device)
+    check(lib().reef_qk_scores_i32_packed(_ptr(q), _ptr(k), B, Hq, Hkv, Sq, Skv, _ptr(acc),
+                                          _ptr(ws), nbytes, _stream()), "qk_scores_i32_packed")
     return acc
 
 

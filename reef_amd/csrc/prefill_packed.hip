@@ -159,6 +159,7 @@ struct PackedArgs {
     int32_t items;      // batch * q_heads * per_head
     int32_t all_precise;
     uint32_t *queue;    // kQueueWords zero-filled words: next item per XCD, then done count
+    int32_t *tap;       // test hook: the exact int32 score of every visible pair, or null
 };
 
 // Two probabilities rounded to fp16 (a packed P operand), and the fp16 of their
@@ -284,6 +285,8 @@ __device__ __forceinline__ PackedArgs uniform_args(const PackedArgs &x) {
     a.q_gran = uni(x.q_gran); a.kv_gran = uni(x.kv_gran); a.kv_tiles = uni(x.kv_tiles);
     a.q_tiles = uni(x.q_tiles); a.per_head = uni(x.per_head); a.items = uni(x.items);
     a.all_precise = uni(x.all_precise);
+    a.queue = uni(x.queue);
+    a.tap = uni(x.tap);
     return a;
 }
 
@@ -302,7 +305,7 @@ __device__ __forceinline__ void keep(const T &x) {
     asm volatile("" ::"v"(x));
 }
 
-template <bool LO, bool FAST>
+template <bool LO, bool FAST, bool TAP = false>
 __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, int b_in, int h_in,
                                                       int tile_in, int8_t *smem_in) {
     const PackedArgs a = uniform_args(args);
@@ -572,6 +575,20 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         __builtin_amdgcn_s_barrier();
         issue_group(j + 2);
         rescale(cur.s, cur.mx);
+        if constexpr (TAP) {
+            // Test hook: tile j's integer scores, read back from the accumulators
+            // relative to s_run, for every key the row sees.
+            int32_t *trow = a.tap + ((int64_t)(b * a.q_heads + h) * a.q_len + row) * a.kv_len;
+            const int kt = kt0 + kPK * j;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kt + 32 * u + 16 * grp + r;
+                    if (row_ok && key >= lo && key <= hi)
+                        trow[key] = cur.s.u[u][r] - kScoreBias + s_run;
+                }
+        }
         const int8_t *sK = kring + ((j + 1) % kSlots) * kKTile;
         const int8_t *sV = vring + (j % kSlots) * kVTile;
         i32x4 kop[2][kPD / 32];
@@ -826,7 +843,10 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(Pac
             packed_tile<LO, FAST>(a, b, h, first, smem);
             if (second >= 0) packed_tile<LO, FAST>(a, b, h, second, smem);
         };
-        if (lo) {
+        if (a.tap) {  // the score hook's launch: one fp16 P, small c (see the entry point)
+            packed_tile<false, true, true>(a, b, h, first, smem);
+            if (second >= 0) packed_tile<false, true, true>(a, b, h, second, smem);
+        } else if (lo) {
             if (fast) run(std::true_type{}, std::true_type{});
             else run(std::true_type{}, std::false_type{});
         } else {
@@ -852,13 +872,12 @@ int64_t packed_image_bytes(int64_t batch, int64_t kv_heads, int64_t kv_len) {
     return img + ceil_div(batch * kv_heads * tiles * 4, 256) * 256;
 }
 
-reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *q,
-                                  const int64_t (&qst)[3], const int8_t *k,
-                                  const int64_t (&kst)[3], const int8_t *v,
-                                  const int64_t (&vst)[3], const float *q_scales,
-                                  const float *k_scales, const float *v_scales, float *out,
-                                  const int64_t (&ost)[3], void *image, uint32_t *queue,
-                                  hipStream_t stream) {
+namespace {
+reef_status packed_launch(const reef_attention_params *p, const int8_t *q, const int64_t (&qst)[3],
+                          const int8_t *k, const int64_t (&kst)[3], const int8_t *v,
+                          const int64_t (&vst)[3], const float *q_scales, const float *k_scales,
+                          const float *v_scales, float *out, const int64_t (&ost)[3], void *image,
+                          uint32_t *queue, int32_t *tap, hipStream_t stream) {
     const int64_t tiles = ceil_div(p->kv_len, kPK);
     const int64_t bkv = p->batch * p->kv_heads;
     if (tiles > 65535 || bkv > 65535) return REEF_UNSUPPORTED;
@@ -912,10 +931,91 @@ reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *
     a.items = (int32_t)items;
     a.all_precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0;
     a.queue = queue;
+    a.tap = tap;
     const int64_t grid = std::min<int64_t>(items, kPerCu * compute_units());
     hipLaunchKernelGGL(prefill_packed_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream,
                        a);
     return launch_status();
 }
 
+__global__ void tap_scales_kernel(float *s) {
+    s[0] = 1.0f;          // q and k: per tensor, unit scale
+    s[1] = 1.0f / 254.0f;  // v: values within 1/2, one fp16 P
+}
+
+// Workspace of the score hook: queue words, the V image, the attention output, scales.
+struct TapLayout {
+    int64_t image, out, scales, total;
+};
+TapLayout tap_layout(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t q_len,
+                     int64_t kv_len) {
+    TapLayout t;
+    t.image = 256;
+    t.out = t.image + ceil_div(packed_image_bytes(batch, kv_heads, kv_len), 256) * 256;
+    t.scales = t.out + ceil_div(batch * q_heads * q_len * kPD * 4, 256) * 256;
+    t.total = t.scales + 256;
+    return t;
+}
+}  // namespace
+
+reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *q,
+                                  const int64_t (&qst)[3], const int8_t *k,
+                                  const int64_t (&kst)[3], const int8_t *v,
+                                  const int64_t (&vst)[3], const float *q_scales,
+                                  const float *k_scales, const float *v_scales, float *out,
+                                  const int64_t (&ost)[3], void *image, uint32_t *queue,
+                                  hipStream_t stream) {
+    return packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out, ost, image,
+                         queue, nullptr, stream);
+}
+
 }  // namespace reef
+
+// Test hook of the packed schedule (head_dim 128): the packed kernel runs one
+// attention over (q, k, v = k) with every row seeing every key (query_start =
+// kv_len - 1), unit q and k scales and a softmax scale small enough for its one-FMA
+// probabilities, and stores the score accumulators of every (query, key) pair as it
+// reads them, relative to its running maximum, back into plain int32 sums.
+extern "C" size_t reef_qk_scores_i32_packed_workspace_bytes(int64_t batch, int64_t q_heads,
+                                                            int64_t kv_heads, int64_t q_len,
+                                                            int64_t kv_len) {
+    if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_len <= 0 || kv_len <= 0) return 0;
+    return (size_t)reef::tap_layout(batch, q_heads, kv_heads, q_len, kv_len).total;
+}
+
+extern "C" reef_status reef_qk_scores_i32_packed(const int8_t *q, const int8_t *k, int64_t batch,
+                                                 int64_t q_heads, int64_t kv_heads, int64_t q_len,
+                                                 int64_t kv_len, int32_t *acc, void *workspace,
+                                                 size_t workspace_bytes, hipStream_t stream) {
+    using namespace reef;
+    if (!q || !k || !acc || !workspace || batch <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+        q_len <= 0 || kv_len <= 0 || q_heads % kv_heads != 0 || !aligned(q, 16) ||
+        !aligned(k, 16) || !aligned(workspace, 256))
+        return REEF_INVALID_ARGUMENT;
+    if (q_len >= (int64_t(1) << 30) || kv_len >= (int64_t(1) << 30)) return REEF_UNSUPPORTED;
+    const TapLayout t = tap_layout(batch, q_heads, kv_heads, q_len, kv_len);
+    if ((int64_t)workspace_bytes < t.total) return REEF_INVALID_ARGUMENT;
+    char *ws = static_cast<char *>(workspace);
+    float *scales = reinterpret_cast<float *>(ws + t.scales);
+    hipLaunchKernelGGL(tap_scales_kernel, dim3(1), dim3(1), 0, stream, scales);
+    if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
+    reef_attention_params p{};
+    p.batch = batch;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.q_len = q_len;
+    p.kv_len = kv_len;
+    p.head_dim = kPD;
+    p.query_start = kv_len - 1;
+    p.window = 0;
+    p.softmax_scale = 1e-3f;
+    p.q_granularity = REEF_SCALE_PER_TENSOR;
+    p.kv_granularity = REEF_SCALE_PER_TENSOR;
+    p.flags = 0;
+    const int64_t qst[3] = {q_heads * q_len * kPD, q_len * kPD, kPD};
+    const int64_t kst[3] = {kv_heads * kv_len * kPD, kv_len * kPD, kPD};
+    const int64_t ost[3] = {q_heads * q_len * kPD, q_len * kPD, kPD};
+    return packed_launch(&p, q, qst, k, kst, k, kst, scales, scales, scales + 1,
+                         reinterpret_cast<float *>(ws + t.out), ost, ws + t.image,
+                         reinterpret_cast<uint32_t *>(ws), acc, stream);
+}

@@ -66,6 +66,33 @@ def test_qk_scores_bit_exact(reef, B, Hq, Hkv, Sq, Skv, D):
     assert np.array_equal(acc[0, 0], oracle.qk_i32(q[0, 0], k[0, 0]))
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv", [
+    (1, 1, 1, 300, 300), (2, 4, 2, 37, 101), (1, 2, 1, 1, 33), (1, 8, 1, 200, 129),
+    (3, 3, 3, 65, 17), (1, 2, 2, 520, 1000)])
+def test_qk_scores_packed_kernel_bit_exact(reef, B, Hq, Hkv, Sq, Skv):
+    """The packed prefill kernel's own score accumulators (its LDS key order, its
+    accumulators relative to the running maximum, rescales included) read back as
+    int32 sums: bit-exact against the integer product, -128 * -128 included, key
+    counts that are not multiples of the 64-key tile."""
+    case(f"qk_scores_i32_packed B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv}")
+    rng = np.random.default_rng(B * 1009 + Sq + Skv)
+    D = 128
+    q = rand_i8(rng, (B, Hq, Sq, D), low=-128)
+    k = rand_i8(rng, (B, Hkv, Skv, D), low=-128)
+    q[0, 0, 0] = -128
+    k[0, 0, 0] = -128
+    if Sq > 1 and Skv > 1:                          # a late maximum forces a rescale
+        k[0, 0, Skv - 1] = 127
+        q[0, 0, 1] = 127
+    acc = host(reef.qk_scores_i32_packed(gpu(q), gpu(k)))
+    g = Hq // Hkv
+    want = np.einsum("bhqd,bhkd->bhqk", q.astype(np.int64),
+                     np.repeat(k, g, axis=1).astype(np.int64))
+    assert np.array_equal(acc, want)
+    assert acc[0, 0, 0, 0] == 128 * 128 * D
+    assert np.array_equal(acc[0, 0], oracle.qk_i32(q[0, 0], k[0, 0]))
+
+
 # --- bit-exact quantization ---------------------------------------------------------------
 
 def _ties(n):
