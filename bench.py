@@ -615,10 +615,53 @@ def cpu_decode_full(oracle, kind, cfg, host, threads):
             "cores": threads, "kind": kind, "sample": "the whole decode step"}
 
 
+def cpu_decode_paged_full(oracle, kind, cfg, lens, host, threads):
+    """Every (sequence, query head) of the ragged paged decode step through the CPU
+    path, each sequence's pages gathered into token order first (outside the timed
+    region): one query row at position L_b - 1 over its L_b cached keys, per-token
+    K/V scales. GB/s of the step's algorithmic bytes."""
+    q, qsc, kp, vp, ksp, vsp, table = host
+    B, Hq, Hkv, D = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim
+    scale = 1.0 / math.sqrt(D)
+    seqs = []
+    for b in range(B):
+        L = int(lens[b])
+        pages = table[b, : (L + 15) // 16]
+        k = kp[pages].transpose(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :L]
+        v = vp[pages].transpose(1, 0, 3, 2).reshape(Hkv, -1, D)[:, :L]  # [P, Hkv, D, 16] pages
+        ks = ksp[pages].transpose(1, 0, 2).reshape(Hkv, -1)[:, :L]
+        vs = vsp[pages].transpose(1, 0, 2).reshape(Hkv, -1)[:, :L]
+        seqs.append(tuple(np.ascontiguousarray(x) for x in (k, v, ks, vs)))
+
+    def job(b):
+        k, v, ks, vs = seqs[b]
+        L = int(lens[b])
+        for h in range(Hq):
+            kvh = h // (Hq // Hkv)
+            if kind == "reference":
+                oracle.ref_attention_int8_head(q[b, h][None], k[kvh], v[kvh],
+                                               np.full(1, qsc[h], np.float32), ks[kvh], vs[kvh],
+                                               L - 1, 0, scale)
+            else:
+                p = oracle.Problem(1, 1, 1, 1, L, D, query_start=L - 1, softmax_scale=scale,
+                                   q_granularity=oracle.GRAN_HEAD,
+                                   kv_granularity=oracle.GRAN_TOKEN)
+                oracle.attention_int8(p, q[b, h][None, None, None], k[kvh][None, None],
+                                      v[kvh][None, None], qsc[h:h + 1], ks[kvh], vs[kvh],
+                                      threads=1)
+        return 0
+    _, t = run_jobs([lambda b=b: job(b) for b in range(B)], threads)
+    nbytes = cfg.kv_bytes(lens)
+    return {"workload": cfg.name, "value": nbytes / t / 1e9, "unit": "GB/s", "seconds": t,
+            "cores": threads, "kind": kind, "sample": "the whole decode step"}
+
+
 def cpu_baselines(torch, reef, W, cfg, inputs, budget_s):
     """The CPU path on this host: a bounded sample of the headline prefill (the
-    record's value), plus the whole 1x32x2048x128 prefill and the whole B64 L4096
-    decode step on the same threads."""
+    record's value), plus the whole 1x32x2048x128 prefill, a bounded sample of the
+    1x8q/1kv x4096x128 prefill (extrapolated to the whole workload), the whole B64
+    L4096 decode step and the whole ragged paged B128 decode step on the same
+    threads."""
     import oracle
     kind = "reference" if oracle.ref_available() else "port"
     model, ncpu = host_cpu()
@@ -638,7 +681,25 @@ def cpu_baselines(torch, reef, W, cfg, inputs, budget_s):
     del q, qsc, k, vp, ksc, vsc, v_tok
     torch.cuda.empty_cache()
     full.append(cpu_decode_full(oracle, kind, c3, host3, threads))
+    del host3
+    c5b, lens5, _, setups5, (q5, qsc5, _) = decode_paged_setup(torch, reef, W, pools=1)
+    host5 = (q5.cpu().numpy(), qsc5.cpu().numpy()) + tuple(t.cpu().numpy() for t in setups5[0])
+    del setups5, q5, qsc5
+    torch.cuda.empty_cache()
+    full.append(cpu_decode_paged_full(oracle, kind, c5b, lens5, host5, threads))
+    del host5
     rec["full_runs"] = full
+    c5a, _, t5, _, _ = prefill_setup(torch, reef, W, "prefill_1x8x4096x128_gqa")
+    s5 = cpu_prefill_sample(oracle, kind, c5a, tuple(t.cpu().numpy() for t in t5), threads,
+                            budget_s / 4)
+    del t5
+    ops5 = c5a.algorithmic_ops()
+    rec["extrapolated_runs"] = [{
+        "workload": c5a.name, "value": s5["value"], "unit": "TOPS", "cores": threads,
+        "kind": kind, "sample": s5["sample"],
+        "seconds_full_workload_extrapolated": ops5 / (s5["value"] * 1e12),
+        "extrapolated_from": "the sample's rate in algorithmic ops, applied to the whole "
+                             "workload's ops"}]
     return rec
 
 
@@ -705,6 +766,11 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
                      "traffic": recorded_traffic(args.prefill),
+                     "traffic_source": f"profiles/{args.prefill}_hbm_traffic.md: rocprofv3 "
+                                       "FETCH_SIZE and WRITE_SIZE per call in a separate "
+                                       "profiling run of the same kernels, each scaled by "
+                                       "what the counter reads for a plain copy of known "
+                                       "size; not measured in this run",
                      "kernel": prefill_kernels(torch, cfg),
                      "kernel_ms": round(kern_ms, 5), "algorithmic_ops_per_launch": ops,
                      "timing": "HIP events on the launch stream around the timed launches; "
