@@ -24,19 +24,10 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "reef_common.hpp"
+#include "prefill_packed.hpp"
 
 namespace reef {
 
-// The packed schedule (prefill_packed.hip).
-int64_t packed_image_bytes(int64_t batch, int64_t kv_heads, int64_t kv_len);
-reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *q,
-                                  const int64_t (&qst)[3], const int8_t *k,
-                                  const int64_t (&kst)[3], const int8_t *v,
-                                  const int64_t (&vst)[3], const float *q_scales,
-                                  const float *k_scales, const float *v_scales, float *out,
-                                  const int64_t (&ost)[3], void *image, uint32_t *queue,
-                                  hipStream_t stream);
 
 namespace {
 
@@ -932,6 +923,7 @@ int64_t stream_items(const reef_attention_params &p) {
 }
 
 int64_t stream_slot_floats() { return StreamSlot<128>::FLOATS; }
+static_assert(StreamSlot<128>::FLOATS == kPartSlotFloats, "the packed schedule's slots");
 
 
 }  // namespace
@@ -1063,13 +1055,29 @@ extern "C" reef_status reef_attention_prefill_int8(
     const bool packed_ok = D == 128 && !tok && workspace &&
                            (int64_t)workspace_bytes >= bal_bytes + packed_bytes(*p);
     if (sched == REEF_ATTN_SCHED_PACKED && !packed_ok) return REEF_INVALID_ARGUMENT;
+    if (sched == REEF_ATTN_SCHED_PACKED && !packed_fits(*p)) return REEF_UNSUPPORTED;
+    // The packed schedule takes whole query tiles from per-XCD queues on grids with
+    // at least one (light, heavy) pair of tiles per compute unit (the library's choice
+    // there), and, forced on smaller grids, equal runs of (tile, key tile) steps with
+    // cut tiles merged through the balanced schedule's counters and slots (one counter
+    // per tile; measured slower than the one-item and balanced kernels there: each
+    // tile call and each merge costs 10-13 us of memory round trips). Outside its
+    // limits AUTO falls back to the other schedules.
+    const bool packed_large = packed_by_default(*p);
+    const bool packed_runs_ok = stream_items(*p) <= kStreamMaxItems;
+    if (sched == REEF_ATTN_SCHED_PACKED && !packed_large && !packed_runs_ok)
+        return REEF_UNSUPPORTED;
     if (sched == REEF_ATTN_SCHED_PACKED ||
-        (sched == REEF_ATTN_SCHED_AUTO && packed_ok && packed_by_default(*p))) {
+        (sched == REEF_ATTN_SCHED_AUTO && packed_ok && packed_fits(*p) && packed_large)) {
         const int64_t qst[3] = {a.q_sb, a.q_sh, a.q_st}, kst[3] = {a.k_sb, a.k_sh, a.k_st},
                       vst[3] = {a.v_sb, a.v_sh, a.v_st}, ost[3] = {a.o_sb, a.o_sh, a.o_st};
+        PackedWork work;
+        work.balanced = !packed_large && packed_runs_ok;
+        work.queue = static_cast<uint32_t *>(workspace) + kStreamMaxItems;
+        work.counters = static_cast<uint32_t *>(workspace);
+        work.slots = reinterpret_cast<float *>(static_cast<char *>(workspace) + kStreamCounterBytes);
         return prefill_packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out,
-                                     ost, static_cast<char *>(workspace) + bal_bytes,
-                                     static_cast<uint32_t *>(workspace) + kStreamMaxItems, stream);
+                                     ost, static_cast<char *>(workspace) + bal_bytes, work, stream);
     }
     // Every schedule splits P into hi + lo where the values need it: always with the
     // precision flag or per-token K/V scales, otherwise per item (two launches, each

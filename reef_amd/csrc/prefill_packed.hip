@@ -9,8 +9,7 @@
 //   * vt_pack_kernel writes, once per call, an fp16 image of V: per (batch, kv head)
 //     and 64-key tile, 128 channel rows of 64 keys (16 KB), the 16-byte chunks of
 //     each row in the bank-swizzled order the P.V operand reads use. Every int8 code
-//     is an fp16 integer, so the image is exact. Beside it, per tile, the largest
-//     |code| in each 32-channel block.
+//     is an fp16 integer, so the image is exact.
 //   * The attention kernel copies K (the caller's int8 rows) and the V image into
 //     LDS with direct-to-LDS buffer loads: a ring of three K slots and one of three
 //     V slots, one barrier per tile, two tiles in flight beyond the one computed.
@@ -20,9 +19,9 @@
 //     fp32 online softmax in base 2 with a lazy rescale, and O^T = V^T . P^T on
 //     v_mfma_f32_32x32x16_f16. The scores of tile j + 1 are issued before tile j's
 //     softmax so the matrix cores and the vector ALU work side by side.
-//   * Precision of P: when any 32-channel value block of a head has dequantized
-//     values above kHiOnlyMax (1), P is split into fp16 hi + lo parts (two products,
-//     22 bits) in every block; otherwise one fp16 P, each off by at most 2^-11 of
+//   * Precision of P: when a head's value scale allows dequantized values above
+//     kHiOnlyMax (127 s_v > 1), P is split into fp16 hi + lo parts (two products, 22
+//     bits) in every block; otherwise one fp16 P, each off by at most 2^-11 of
 //     itself, moves an output by at most 2^-11 max|v_j - out| < 1e-3. The
 //     probabilities carry an exponent offset (kShift) that keeps them out of the fp16
 //     subnormals, and the row sums are of exactly the P parts the products use.
@@ -32,23 +31,15 @@
 //     in a queue its workgroups take from as they finish, then the other XCDs'
 //     queues; the last heads of a share come as single tiles, heaviest first. The
 //     light tile of a pair runs first: its keys are a prefix of the heavy one's.
+//     Grids with fewer pairs than compute units take the balanced form instead:
+//     equal runs of (query tile, key tile) steps per workgroup, cut tiles merged.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
 
-#include "reef_common.hpp"
+#include "prefill_packed.hpp"
 
 namespace reef {
-
-// Host side, used by prefill.hip's entry point.
-int64_t packed_image_bytes(int64_t batch, int64_t kv_heads, int64_t kv_len);
-reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *q,
-                                  const int64_t (&qst)[3], const int8_t *k,
-                                  const int64_t (&kst)[3], const int8_t *v,
-                                  const int64_t (&vst)[3], const float *q_scales,
-                                  const float *k_scales, const float *v_scales, float *out,
-                                  const int64_t (&ost)[3], void *image, uint32_t *queue,
-                                  hipStream_t stream);
 
 namespace {
 
@@ -68,6 +59,19 @@ constexpr int kVBlocks = kVTile / 1024 / kWaves;  //                            
 constexpr int kXcdCount = 8;               // workgroup i of a launch runs on XCD i % 8
 constexpr int kPerCu = 2;                  // resident workgroups per compute unit (2 x 72 KB)
 constexpr int kQueueWords = kXcdCount + 1;
+// The part a tile call computes, written to LDS by the kernel before the call (read
+// there rather than passed: extra arguments of the called tile function cost it the
+// address space of its LDS pointers or a save of its registers): key tiles [c0, c1)
+// of the query tile, and the part slot its unnormalized result goes to (-1: the
+// whole tile, normalized into the output).
+struct PartInfo {
+    int32_t c0, c1, slot, pad;
+};
+constexpr int kSmem = kKRing + kVRing + (int)sizeof(PartInfo);
+// A part slot (8-byte words): per wave and lane, the 64 accumulators in register
+// order, then (running maximum, row sum); word e of wave w, lane l at [(w E + e) 64 + l].
+constexpr int kSlotWords = kWaves * 33 * 64;
+static_assert(2 * kSlotWords == kPartSlotFloats, "a part slot of the balanced schedule");
 
 // Position of 16-byte chunk c in a 128-byte LDS row r: the 16 lanes that read
 // chunk c of 16 consecutive rows land in 16 distinct bank groups.
@@ -84,7 +88,6 @@ struct PackArgs {
     int64_t v_sb, v_sh, v_st;
     int32_t kv_heads, kv_len, tiles;
     int8_t *img;      // [B * Hkv][tiles][kVTile]
-    uint32_t *bmax;   // [B * Hkv][tiles]: byte i = max |code| of channels 32i .. 32i + 31
 };
 
 // One workgroup per (tile, batch x kv head).
@@ -92,8 +95,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(PackArgs a) {
     constexpr int kRow = kPD + 4;  // LDS bytes per key row: column reads 8 rows apart
                                    // fall in 8 distinct banks
     __shared__ __attribute__((aligned(16))) int8_t sV[kPK * kRow];
-    __shared__ uint32_t sMax[4][4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const int tile = blockIdx.x, bkv = blockIdx.y;
     const int b = bkv / a.kv_heads, h = bkv % a.kv_heads;
     const int kt = tile * kPK;
@@ -112,41 +114,19 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(PackArgs a) {
     }
     __syncthreads();
     int8_t *dst = a.img + ((int64_t)bkv * a.tiles + tile) * kVTile;
-    uint32_t mx[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         // image chunk s: channel m, position s % 8 holding keys 8c .. 8c + 7
         const int s = tid + 256 * i, m = s >> 3, c = swz(m, s & 7);
         f16x8 o;
-        int big = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int code = sV[(8 * c + e) * kRow + m];
-            o[e] = (_Float16)code;
-            big = max(big, code < 0 ? -code : code);
-        }
+        for (int e = 0; e < 8; ++e) o[e] = (_Float16)sV[(8 * c + e) * kRow + m];
         *reinterpret_cast<f16x8 *>(dst + 16 * s) = o;
-        mx[i] = wave_max_u32((uint32_t)big);  // chunk i of every thread is channel block i
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sMax[wave][i] = mx[i];
-    }
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t m = max(max(sMax[0][i], sMax[1][i]), max(sMax[2][i], sMax[3][i]));
-            word |= m << (8 * i);
-        }
-        a.bmax[(int64_t)bkv * a.tiles + tile] = word;
     }
 }
 
 struct PackedArgs {
     const int8_t *q, *k, *img;
-    const uint32_t *bmax;
     const float *qs, *ks, *vs;
     float *out;
     int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, o_sb, o_sh, o_st;
@@ -160,6 +140,7 @@ struct PackedArgs {
     int32_t all_precise;
     uint32_t *queue;    // kQueueWords zero-filled words: next item per XCD, then done count
     int32_t *tap;       // test hook: the exact int32 score of every visible pair, or null
+    uint64_t *slots;    // balanced: part slots (kSlotWords words each)
 };
 
 // Two probabilities rounded to fp16 (a packed P operand), and the fp16 of their
@@ -274,7 +255,7 @@ __device__ __forceinline__ T *uni(T *p) {
 
 __device__ __forceinline__ PackedArgs uniform_args(const PackedArgs &x) {
     PackedArgs a;
-    a.q = uni(x.q); a.k = uni(x.k); a.img = uni(x.img); a.bmax = uni(x.bmax);
+    a.q = uni(x.q); a.k = uni(x.k); a.img = uni(x.img);
     a.qs = uni(x.qs); a.ks = uni(x.ks); a.vs = uni(x.vs); a.out = uni(x.out);
     a.q_sb = uni(x.q_sb); a.q_sh = uni(x.q_sh); a.q_st = uni(x.q_st);
     a.k_sb = uni(x.k_sb); a.k_sh = uni(x.k_sh); a.k_st = uni(x.k_st);
@@ -287,8 +268,15 @@ __device__ __forceinline__ PackedArgs uniform_args(const PackedArgs &x) {
     a.all_precise = uni(x.all_precise);
     a.queue = uni(x.queue);
     a.tap = uni(x.tap);
+    a.slots = uni(x.slots);
     return a;
 }
+
+// LDS views of the tile function's ring pointers: written as such, every operand read
+// is a ds_read whatever the compiler infers across the calls.
+typedef __attribute__((address_space(3))) int8_t lds_i8;
+typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
 
 #define REEF_SLOT() __builtin_amdgcn_sched_barrier(0)
 // Empty asm statements that hold a vector value in place: pin() makes the value
@@ -310,7 +298,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
                                                       int tile_in, int8_t *smem_in) {
     const PackedArgs a = uniform_args(args);
     const int b = uni(b_in), h = uni(h_in), tile = uni(tile_in);
-    int8_t *const smem = uni(smem_in);
+    lds_i8 *const smem = (lds_i8 *)uni(smem_in);
     constexpr int DB = kPD / 32;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -331,7 +319,12 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     const int key_lo = a.window > 0 ? max(0, a.query_start + q0 + 1 - a.window) : 0;
     const int key_hi = min(a.query_start + r_last, a.kv_len - 1);
     const int kt0 = key_lo / kPK * kPK;
-    const int n_tiles = (key_hi - kt0) / kPK + 1;
+    // This call's key tiles [j_lo, n_tiles) of the query tile's, and its part slot.
+    const __attribute__((address_space(3))) PartInfo *part =
+        (const __attribute__((address_space(3))) PartInfo *)(smem + kKRing + kVRing);
+    const int n_tiles = min(uni(part->c1), (key_hi - kt0) / kPK + 1);
+    const int j_lo = uni(part->c0);
+    const int slot = uni(part->slot);
 
     // Query operand and scales (independent loads, issued before the tile loads).
     i32x4 qop[kPD / 32];
@@ -364,12 +357,12 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     for (int i = 0; i < kVBlocks; ++i) voff[i] = (uint32_t)(16 * (64 * (wave + kWaves * i) + lane));
     const int8_t *kbase = a.k + b * a.k_sb + kvh * a.k_sh;
     const int8_t *ibase = a.img + ((int64_t)(b * a.kv_heads + kvh) * a.kv_tiles) * kVTile;
-    int8_t *kring = smem, *vring = smem + kKRing;
+    lds_i8 *kring = smem, *vring = smem + kKRing;
     auto issue_k = [&](int j) {  // K of tile j into K slot j % 3; rows past kv_len read zeros
         const int kt = kt0 + kPK * j;
         const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(
             kbase + (int64_t)kt * a.k_st, (uint32_t)((int64_t)(a.kv_len - 1 - kt) * a.k_st + kPD));
-        int8_t *st = kring + (j % kSlots) * kKTile;
+        lds_i8 *st = kring + (j % kSlots) * kKTile;
 #pragma unroll
         for (int i = 0; i < kKBlocks; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -379,7 +372,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     auto issue_v = [&](int j) {  // V image of tile j into V slot j % 3
         const __amdgpu_buffer_rsrc_t vr =
             buffer_rsrc(ibase + (int64_t)(kt0 / kPK + j) * kVTile, kVTile);
-        int8_t *st = vring + (j % kSlots) * kVTile;
+        lds_i8 *st = vring + (j % kSlots) * kVTile;
 #pragma unroll
         for (int i = 0; i < kVBlocks; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -549,18 +542,18 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         Scores s;
         int32_t mx;  // this lane's maximum of s
     };
-    // Scores of tile 0 (the prologue; later tiles' scores come from step()).
+    // Scores of tile j_lo (the prologue; later tiles' scores come from step()).
     auto first_scores = [&]() {
         Tile t;
-        const int8_t *sK = kring;
+        const lds_i8 *sK = kring + (j_lo % kSlots) * kKTile;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int tt = 0; tt < kPD / 32; ++tt) {
-                const i32x4 kop = *reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[tt]);
+                const i32x4 kop = *reinterpret_cast<const lds_i32x4 *>(sK + 4096 * u + kpos[tt]);
                 t.s.u[u] = mfma_32x32x32_i8(kop, qop[tt], tt == 0 ? bias : t.s.u[u]);
             }
-        mask_scores(t.s, 0);
+        mask_scores(t.s, j_lo);
         t.mx = lane_max(t.s);
         return t;
     };
@@ -589,19 +582,19 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
                         trow[key] = cur.s.u[u][r] - kScoreBias + s_run;
                 }
         }
-        const int8_t *sK = kring + ((j + 1) % kSlots) * kKTile;
-        const int8_t *sV = vring + (j % kSlots) * kVTile;
+        const lds_i8 *sK = kring + ((j + 1) % kSlots) * kKTile;
+        const lds_i8 *sV = vring + (j % kSlots) * kVTile;
         i32x4 kop[2][kPD / 32];
         f16x8 vop[4][DB];
         uint32_t ph[4][4], pl[4][4];
         Tile nx;
         auto kread = [&](int u, int t) {
-            kop[u][t] = *reinterpret_cast<const i32x4 *>(sK + 4096 * u + kpos[t]);
+            kop[u][t] = *reinterpret_cast<const lds_i32x4 *>(sK + 4096 * u + kpos[t]);
         };
         auto vread = [&](int cc) {
 #pragma unroll
             for (int d = 0; d < DB; ++d)
-                vop[cc][d] = *reinterpret_cast<const f16x8 *>(sV + 4096 * d + vpos[cc]);
+                vop[cc][d] = *reinterpret_cast<const lds_f16x8 *>(sV + 4096 * d + vpos[cc]);
         };
         auto qk = [&](int u, int t) {
             nx.s.u[u] = mfma_32x32x32_i8(kop[u][t], qop[t], t == 0 ? bias : nx.s.u[u]);
@@ -686,22 +679,23 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         return nx;
     };
 
-    issue_k(0);
-    issue_group(0);
-    issue_group(1);
-    wait_loads(group_loads(0) + group_loads(1));
+    issue_k(j_lo);
+    issue_group(j_lo);
+    issue_group(j_lo + 1);
+    wait_loads(group_loads(j_lo) + group_loads(j_lo + 1));
     __builtin_amdgcn_s_barrier();
     Tile tl = first_scores();
-    // Tiles [it_a, it_b) are whole for every row of the workgroup: no masks.
+    // Tiles [it_a, it_b) are whole for every row of the workgroup: no masks (segment
+    // ends clamped to this call's tiles).
     const int wg_full_lo = a.window > 0 ? a.query_start + r_last + 1 - a.window : 0;
     const int wg_full_hi = min(a.query_start + q0, a.kv_len - 1);
-    const int it_a = max(0, wg_full_lo - kt0 + kPK - 1) / kPK;
     const int span = wg_full_hi + 1 - kt0;
+    const int it_a = max(j_lo, min(n_tiles, max(0, wg_full_lo - kt0 + kPK - 1) / kPK));
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kPK : 0));
     // Two tiles per iteration: the loop-carried scores come back in the registers
     // they left, with no copies.
     // Tile j + 1 needs its scores masked only when it lies outside [it_a, it_b).
-    int j = 0;
+    int j = j_lo;
     auto run = [&](const int end, auto masked_tag, auto mask_next_tag) {
         for (; j + 1 < end; j += 2) {
             Tile mid = step(j, masked_tag, mask_next_tag, tl);
@@ -718,7 +712,28 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     run(n_tiles, std::true_type{}, std::true_type{});
 
     const float l_row = row_sum_of_lane(rs, lane) + (LO ? xor32_sum(l_lo) : 0.0f);
-    if (row_ok) {
+    if (slot >= 0) {
+        // A part of the query tile: its unnormalized accumulators and (s_run, row sum),
+        // every lane (rows past q_len hold finite values), with device-coherent stores
+        // (written through beneath the per-XCD L2s) that complete before the barrier
+        // below. The merge reads them the same way.
+        uint64_t *so = a.slots + (int64_t)slot * kSlotWords;
+        auto put = [&](int e, uint64_t v) {
+            __hip_atomic_store(so + (wave * 33 + e) * 64 + lane, v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        };
+        auto pack2 = [](float x, float y) {
+            return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+        };
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) put(8 * d + e, pack2(acc[d][2 * e], acc[d][2 * e + 1]));
+        put(32, (uint64_t)(uint32_t)s_run | ((uint64_t)__float_as_uint(l_row) << 32));
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);  // every slot store has completed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    } else if (row_ok) {
         float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
         const float norm = cv / l_row;
 #pragma unroll
@@ -736,27 +751,12 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     __syncthreads();
 }
 
-// Whether P needs hi + lo parts for (batch, kv head): some dequantized value of the
-// head reaches above kHiOnlyMax (the largest |code| of each 32-channel block over
-// the head's tiles, times the value scale). Uniform over the workgroup.
-__device__ __forceinline__ bool needs_lo(const PackedArgs &a, int b, int kvh, uint32_t *sRed) {
+// Whether P needs hi + lo parts for (batch, kv head): its value scale allows
+// dequantized magnitudes above kHiOnlyMax (the same rule as the other prefill
+// schedules: 127 s_v, the largest magnitude the engine's quantize_int8 produces).
+__device__ __forceinline__ bool needs_lo(const PackedArgs &a, int b, int kvh) {
     if (a.all_precise) return true;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t *bm = a.bmax + (int64_t)(b * a.kv_heads + kvh) * a.kv_tiles;
-    uint32_t m = 0;
-    for (int t = tid; t < a.kv_tiles; t += 64 * kWaves) {
-        const uint32_t w = bm[t];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) m = max(m, (w >> (8 * i)) & 0xffu);
-    }
-    m = wave_max_u32(m);
-    if (lane == 0) sRed[wave] = m;
-    __syncthreads();
-    uint32_t top = 0;
-    for (int w = 0; w < kWaves; ++w) top = max(top, sRed[w]);
-    __syncthreads();  // sRed is reused by the next item
-    const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-    return __builtin_amdgcn_readfirstlane((int)((float)top * cv > kHiOnlyMax)) != 0;
+    return 127.0f * scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) > kHiOnlyMax;
 }
 
 // XCD y's share of the work: the (batch, head) pairs [bh0, bh0 + nh), an eighth of
@@ -790,10 +790,11 @@ __device__ __forceinline__ Share share_of(const PackedArgs &a, int y) {
 // box, and no run slower than 2.2 ms). The last workgroup to finish resets the
 // queue to zero for the next call.
 __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(PackedArgs a) {
-    __shared__ __attribute__((aligned(1024))) int8_t smem[kKRing + kVRing];
-    __shared__ uint32_t sRed[4 * kWaves];
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kSmem];
     __shared__ int sUnit[2];  // XCD share and unit, or -1
     const int x = blockIdx.x % kXcdCount;
+    if (threadIdx.x == 0)  // every call computes a whole query tile (ordered by the first barrier)
+        *reinterpret_cast<PartInfo *>(smem + kKRing + kVRing) = PartInfo{0, INT32_MAX, -1, 0};
     int tried = 0;  // queues found empty, own XCD's first
     auto take = [&](int &share) -> int {  // thread 0: the next unit, or -1 when all are taken
         while (tried < kXcdCount) {
@@ -828,7 +829,7 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(Pac
         }
         const int b = bh / a.q_heads, h = bh % a.q_heads;
         const int kvh = h / (a.q_heads / a.kv_heads);
-        const bool lo = needs_lo(a, b, kvh, sRed);
+        const bool lo = needs_lo(a, b, kvh);
         // One FMA per probability when the score factor c is small enough that
         // 12582912 c rounds within 1/4 (any q scale granularity but per token, where c
         // varies by row).
@@ -864,12 +865,201 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(Pac
     }
 }
 
+// Steps of the balanced form: a step is (query tile, 64-key tile). Key tiles of query
+// tile `tile`, and their sum over the tiles before T (each of them 128 rows; a window
+// drops a prefix of keys), in closed form.
+__host__ __device__ inline int64_t floor_div64(int64_t x, int64_t y) {  // y > 0
+    return x >= 0 ? x / y : -((-x + y - 1) / y);
+}
+__host__ __device__ inline int64_t tile_key_tiles(int64_t q_len, int64_t kv_len, int64_t qstart,
+                                                  int64_t window, int64_t tile) {
+    const int64_t q0 = tile * kBM;
+    const int64_t r_last = (q0 + kBM < q_len ? q0 + kBM : q_len) - 1;
+    int64_t key_lo = window > 0 ? qstart + q0 + 1 - window : 0;
+    if (key_lo < 0) key_lo = 0;
+    const int64_t key_hi = (qstart + r_last < kv_len - 1 ? qstart + r_last : kv_len - 1);
+    return (key_hi - key_lo / kPK * kPK) / kPK + 1;
+}
+__host__ __device__ inline int64_t key_tiles_before(int64_t qstart, int64_t window, int64_t T) {
+    // Without a window tile t has 2t + 1 + floor((qstart + 127) / 64) key tiles.
+    int64_t s = T + T * (T - 1) + ((qstart + 127) / kPK) * T;
+    if (window > 0) {
+        int64_t t0 = floor_div64(window - qstart - 1, kBM) + 1;
+        if (t0 < 0) t0 = 0;
+        if (T > t0) s -= (T - t0) * (T + t0 - 1) + floor_div64(qstart + 1 - window, kPK) * (T - t0);
+    }
+    return s;
+}
+
+struct BalArgs {
+    int64_t units;       // steps of all query tiles
+    int64_t per_head;    // steps of one (batch, head)
+    uint32_t *counters;  // one per query tile, zero between launches
+};
+
+// The last part of a cut query tile: every part's accumulators and (s_run, row sum)
+// from its slot (this part's too), folded in part order, so the output does not
+// depend on which part finished last.
+__device__ void merge_parts(const PackedArgs &a, int b, int h, int tile, int parts, int first_wg,
+                            int64_t item_u0, int64_t units) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, grp = lane >> 5;
+    const int kvh = h / (a.q_heads / a.kv_heads);
+    const int row = tile * kBM + wave * 32 + col;
+    const bool row_ok = row < a.q_len;
+    const int G = gridDim.x;
+    const float ck = scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
+    const float c = cq * ck * a.score_scale;
+    auto get = [](const uint64_t *p) {
+        return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    };
+    // Part p is logical workgroup first_wg + p; the first part sits in that
+    // workgroup's second slot when its range began before this tile.
+    auto slot_of = [&](int p) {
+        const int lp = first_wg + p;
+        const bool second = p == 0 && (int64_t)lp * units / G < item_u0;
+        return a.slots + (int64_t)(2 * lp + (second ? 1 : 0)) * kSlotWords + wave * 33 * 64 + lane;
+    };
+    // One pass: a running maximum of the parts' s_run with explicit fused
+    // multiply-adds, the next part's loads in flight while this one is folded.
+    uint64_t cur[33], nxt[33];
+    auto fetch = [&](uint64_t(&v)[33], int p) {
+        const uint64_t *sl = slot_of(p);
+#pragma unroll
+        for (int e = 0; e < 33; ++e) v[e] = get(sl + e * 64);
+    };
+    auto lo32 = [](uint64_t w) { return __uint_as_float((uint32_t)w); };
+    auto hi32 = [](uint64_t w) { return __uint_as_float((uint32_t)(w >> 32)); };
+    fetch(cur, 0);
+    int32_t m = 0;
+    float l = 0.0f;
+    f32x16 tot[kPD / 32];
+#pragma unroll
+    for (int d = 0; d < kPD / 32; ++d) tot[d] = f32x16{};
+    for (int p = 0; p < parts; ++p) {
+        if (p + 1 < parts) fetch(nxt, p + 1);
+        const int32_t sp = (int32_t)(uint32_t)cur[32];
+        const int32_t mn = p == 0 ? sp : max(m, sp);
+        const float er = p == 0 ? 0.0f : __builtin_amdgcn_exp2f((float)(m - mn) * c);
+        const float ep = __builtin_amdgcn_exp2f((float)(sp - mn) * c);
+        l = __builtin_fmaf(ep, hi32(cur[32]), l * er);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const int d = e / 8, i = 2 * (e % 8);
+            tot[d][i] = __builtin_fmaf(ep, lo32(cur[e]), tot[d][i] * er);
+            tot[d][i + 1] = __builtin_fmaf(ep, hi32(cur[e]), tot[d][i + 1] * er);
+        }
+        m = mn;
+#pragma unroll
+        for (int e = 0; e < 33; ++e) cur[e] = nxt[e];
+    }
+    if (!row_ok) return;
+    float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
+    const float norm = cv / l;
+#pragma unroll
+    for (int d = 0; d < kPD / 32; ++d) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            f32x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = tot[d][4 * jj + i] * norm;
+            *reinterpret_cast<f32x4 *>(orow + 32 * d + 8 * jj + 4 * grp) = o;
+        }
+    }
+}
+
+// Balanced form for grids with fewer query-tile pairs than compute units: the steps
+// of all query tiles ((batch, head), then tile, then key tile) are cut into G equal
+// runs, one per workgroup, logical workgroup L holding [L units / G, (L + 1) units /
+// G); the G / 8 workgroups of one XCD (hardware workgroup g runs on XCD g % 8) hold
+// consecutive L, so an XCD's L2 sees a few heads. A query tile that a run boundary
+// cuts is computed in parts: each part leaves its unnormalized result in a slot, and
+// the part that counts in last (a counter per query tile) merges them. The counting
+// protocol is the balanced prefill's and the decode merge's: slot stores are
+// device-coherent and complete before the barrier that precedes the relaxed
+// agent-scope increment; the merging part reads the slots after its increment
+// returned.
+__global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_bal_kernel(PackedArgs a,
+                                                                                 BalArgs ba) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[kSmem];
+    __shared__ uint32_t sTicket;
+    PartInfo *sPart = reinterpret_cast<PartInfo *>(smem + kKRing + kVRing);
+    const int G = gridDim.x, g = blockIdx.x;
+    const int x = g % kXcdCount, per = G / kXcdCount, rem = G % kXcdCount;
+    const int L = x * per + min(x, rem) + g / kXcdCount;
+    int64_t u = (int64_t)L * ba.units / G;
+    const int64_t u_end = (int64_t)(L + 1) * ba.units / G;
+    // The first step: (batch, head), then the query tile by bisection over the
+    // closed-form prefix sums (the grid has at most one workgroup per step).
+    int bh = (int)(u / ba.per_head);
+    const int64_t r0 = u - (int64_t)bh * ba.per_head;
+    int lo = 0, hi = a.q_tiles - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (key_tiles_before(a.query_start, a.window, mid) <= r0) lo = mid;
+        else hi = mid - 1;
+    }
+    int tile = lo;
+    int c0 = (int)(r0 - key_tiles_before(a.query_start, a.window, tile));
+    auto wg_of = [&](int64_t unit) { return (int)(((unit + 1) * G - 1) / ba.units); };
+    bool first = true;
+    while (u < u_end) {
+        const int n = (int)tile_key_tiles(a.q_len, a.kv_len, a.query_start, a.window, tile);
+        const int c1 = (int)(c0 + (u_end - u) < n ? c0 + (u_end - u) : n);
+        const int64_t item_u0 = u - c0;
+        const int first_wg = wg_of(item_u0);
+        const int parts = wg_of(item_u0 + n - 1) - first_wg + 1;
+        const int b = bh / a.q_heads, h = bh % a.q_heads;
+        const int kvh = h / (a.q_heads / a.kv_heads);
+        if (threadIdx.x == 0)
+            *sPart = PartInfo{c0, c1, parts > 1 ? 2 * L + (first ? 0 : 1) : -1, 0};
+        __syncthreads();
+        const bool lo_p = needs_lo(a, b, kvh);
+        const float c_item = a.q_gran == REEF_SCALE_PER_TOKEN
+                                 ? INFINITY
+                                 : scale_at(a.qs, a.q_gran, b, h, 0, a.q_heads, a.q_len) *
+                                       scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) *
+                                       a.score_scale;
+        const bool fast = c_item <= kFastCMax;
+        if (lo_p) {
+            if (fast) packed_tile<true, true>(a, b, h, tile, smem);
+            else packed_tile<true, false>(a, b, h, tile, smem);
+        } else {
+            if (fast) packed_tile<false, true>(a, b, h, tile, smem);
+            else packed_tile<false, false>(a, b, h, tile, smem);
+        }
+        if (parts > 1) {
+            // The tile call ended with a barrier after every slot store completed.
+            if (threadIdx.x == 0)
+                sTicket = __hip_atomic_fetch_add(ba.counters + (int64_t)bh * a.q_tiles + tile, 1u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            if (sTicket == (uint32_t)(parts - 1)) {
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                if (threadIdx.x == 0)  // ready for the next launch
+                    __hip_atomic_store(ba.counters + (int64_t)bh * a.q_tiles + tile, 0u,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                merge_parts(a, b, h, tile, parts, first_wg, item_u0, ba.units);
+            }
+        }
+        u += c1 - c0;
+        c0 = 0;
+        first = false;
+        if (++tile == a.q_tiles) {
+            tile = 0;
+            ++bh;
+        }
+        __syncthreads();  // sPart and sTicket are written again for the next tile
+    }
+}
+
 }  // namespace
 
 int64_t packed_image_bytes(int64_t batch, int64_t kv_heads, int64_t kv_len) {
-    const int64_t tiles = ceil_div(kv_len, kPK);
-    const int64_t img = batch * kv_heads * tiles * kVTile;
-    return img + ceil_div(batch * kv_heads * tiles * 4, 256) * 256;
+    return batch * kv_heads * ceil_div(kv_len, kPK) * kVTile;
 }
 
 namespace {
@@ -877,10 +1067,10 @@ reef_status packed_launch(const reef_attention_params *p, const int8_t *q, const
                           const int8_t *k, const int64_t (&kst)[3], const int8_t *v,
                           const int64_t (&vst)[3], const float *q_scales, const float *k_scales,
                           const float *v_scales, float *out, const int64_t (&ost)[3], void *image,
-                          uint32_t *queue, int32_t *tap, hipStream_t stream) {
+                          const PackedWork &work, int32_t *tap, hipStream_t stream) {
+    if (!packed_fits(*p)) return REEF_UNSUPPORTED;
     const int64_t tiles = ceil_div(p->kv_len, kPK);
     const int64_t bkv = p->batch * p->kv_heads;
-    if (tiles > 65535 || bkv > 65535) return REEF_UNSUPPORTED;
     PackArgs pa;
     pa.v = v;
     pa.v_sb = vst[0];
@@ -890,7 +1080,6 @@ reef_status packed_launch(const reef_attention_params *p, const int8_t *q, const
     pa.kv_len = (int32_t)p->kv_len;
     pa.tiles = (int32_t)tiles;
     pa.img = static_cast<int8_t *>(image);
-    pa.bmax = reinterpret_cast<uint32_t *>(static_cast<int8_t *>(image) + bkv * tiles * kVTile);
     hipLaunchKernelGGL(vt_pack_kernel, dim3((unsigned)tiles, (unsigned)bkv), dim3(256), 0, stream,
                        pa);
     if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
@@ -899,7 +1088,6 @@ reef_status packed_launch(const reef_attention_params *p, const int8_t *q, const
     a.q = q;
     a.k = k;
     a.img = pa.img;
-    a.bmax = pa.bmax;
     a.qs = q_scales;
     a.ks = k_scales;
     a.vs = v_scales;
@@ -927,11 +1115,23 @@ reef_status packed_launch(const reef_attention_params *p, const int8_t *q, const
     a.q_tiles = (int32_t)ceil_div(p->q_len, kBM);
     a.per_head = (a.q_tiles + 1) / 2;
     const int64_t items = (int64_t)a.per_head * p->batch * p->q_heads;
-    if (items >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
     a.items = (int32_t)items;
     a.all_precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0;
-    a.queue = queue;
+    a.queue = work.queue;
     a.tap = tap;
+    a.slots = reinterpret_cast<uint64_t *>(work.slots);
+    if (work.balanced && !tap) {
+        BalArgs ba;
+        ba.per_head = key_tiles_before(p->query_start, p->window, a.q_tiles - 1) +
+                      tile_key_tiles(p->q_len, p->kv_len, p->query_start, p->window, a.q_tiles - 1);
+        ba.units = ba.per_head * p->batch * p->q_heads;
+        ba.counters = work.counters;
+        // At most one workgroup per step, so that every run holds a step.
+        const int64_t grid = std::min<int64_t>(ba.units, kPerCu * compute_units());
+        hipLaunchKernelGGL(prefill_packed_bal_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0,
+                           stream, a, ba);
+        return launch_status();
+    }
     const int64_t grid = std::min<int64_t>(items, kPerCu * compute_units());
     hipLaunchKernelGGL(prefill_packed_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, stream,
                        a);
@@ -963,10 +1163,16 @@ reef_status prefill_packed_launch(const reef_attention_params *p, const int8_t *
                                   const int64_t (&kst)[3], const int8_t *v,
                                   const int64_t (&vst)[3], const float *q_scales,
                                   const float *k_scales, const float *v_scales, float *out,
-                                  const int64_t (&ost)[3], void *image, uint32_t *queue,
+                                  const int64_t (&ost)[3], void *image, const PackedWork &work,
                                   hipStream_t stream) {
     return packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out, ost, image,
-                         queue, nullptr, stream);
+                         work, nullptr, stream);
+}
+
+bool packed_fits(const reef_attention_params &p) {
+    const int64_t tiles = ceil_div(p.kv_len, kPK);
+    const int64_t items = (ceil_div(p.q_len, kBM) + 1) / 2 * p.batch * p.q_heads;
+    return tiles <= 65535 && p.batch * p.kv_heads <= 65535 && items < (int64_t(1) << 31);
 }
 
 }  // namespace reef
@@ -1017,5 +1223,6 @@ extern "C" reef_status reef_qk_scores_i32_packed(const int8_t *q, const int8_t *
     const int64_t ost[3] = {q_heads * q_len * kPD, q_len * kPD, kPD};
     return packed_launch(&p, q, qst, k, kst, k, kst, scales, scales, scales + 1,
                          reinterpret_cast<float *>(ws + t.out), ost, ws + t.image,
-                         reinterpret_cast<uint32_t *>(ws), acc, stream);
+                         PackedWork{false, reinterpret_cast<uint32_t *>(ws), nullptr, nullptr}, acc,
+                         stream);
 }

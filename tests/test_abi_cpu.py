@@ -78,9 +78,9 @@ def test_prefill_workspace_bytes_and_alignment():
     # a fixed region of 65536 counters (item counters and the packed queue), then two partial slots per workgroup, two
     # workgroups per compute unit (256 without a GPU): 128 x 128 outputs plus (max,
     # sum) of 128 rows; then the packed value image: 32 tiles of 64 keys per head,
-    # 16 KB each, and one 4-byte block maximum per tile
+    # 16 KB each
     balanced = 65536 * 4 + 2 * 512 * (128 * 128 + 2 * 256) * 4
-    image = 32 * 32 * 16384 + 32 * 32 * 4
+    image = 32 * 32 * 16384
     assert n == balanced + image
     p64 = good_params(batch=1, q_heads=32, kv_heads=32, q_len=2048, kv_len=2048, head_dim=64)
     # the same balanced region (slots sized for head_dim 128, so that every shape finds

@@ -598,6 +598,32 @@ def test_prefill_rejects_bad_arguments(reef):
         reef.attention_prefill(zz, zz, zz, s, s, s)
 
 
+def test_prefill_auto_falls_back_outside_packed_limits(reef):
+    """2048 sequences x 32 heads of 128 tokens: 65536 (batch, kv head) pairs, one past
+    the packed schedule's 16-bit launch dimension. The library's choice (the packed
+    schedule for a grid this large) falls back to the one-item kernel and matches the
+    oracle; forcing the packed schedule reports REEF_UNSUPPORTED."""
+    B, H, S, D = 2048, 32, 128, 128
+    case(f"prefill B{B} H{H} S{S}: past the packed schedule's grid limits")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    q, k, v = (torch.randint(-127, 128, (B, H, S, D), dtype=torch.int8, device="cuda",
+                             generator=g) for _ in range(3))
+    sc = torch.full((H,), 0.02, dtype=torch.float32, device="cuda")
+    out = reef.attention_prefill(q, k, v, sc, sc, sc)
+    with pytest.raises(reef.Unsupported):
+        reef.attention_prefill(q, k, v, sc, sc, sc, schedule=reef.SCHED_PACKED)
+    p = oracle.Problem(1, 1, 1, S, S, D, softmax_scale=1 / math.sqrt(D), q_granularity=1,
+                       kv_granularity=1)
+    one = np.full(1, 0.02, np.float32)
+    for b, h in ((0, 0), (1023, 17), (2047, 31)):
+        sl = lambda t: host(t[b:b + 1, h:h + 1])  # noqa: E731
+        gold = oracle.attention_int8(p, sl(q), sl(k), sl(v), one, one, one)
+        err = float(np.abs(host(out[b:b + 1, h:h + 1]) - gold).max())
+        print(f"b{b} h{h} max_abs_err {err:.3e}", flush=True)
+        assert err <= TOL, (b, h, err)
+
+
 # --- decode ----------------------------------------------------------------------------------
 
 def _decode_problem(B, Hq, Hkv, D, lens, seed, max_ctx):
