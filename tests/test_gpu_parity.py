@@ -238,6 +238,24 @@ def test_quantize_streams_beyond_the_cache(reef):
     assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
 
 
+def test_quantize_per_head_groups_beyond_the_cache(reef):
+    """Per-head scales of a 436 MB stream (the two-pass kernels with non-temporal
+    loads), 13 heads of 33.5 MB with a large outlier in the last value of the last
+    head: bit-exact against the oracle."""
+    import torch
+    shape = (2, 13, 4096, 1024)
+    case(f"quantize_per_head {list(shape)}, 436 MB")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(37)
+    xd = torch.randn(shape, generator=g, device="cuda")
+    xd[1, 12, 4095, 1023] = 900.0
+    q, s = reef.quantize_per_head(xd)
+    x = host(xd)
+    qo, so = oracle.quantize_per_head(x)
+    assert np.array_equal(host(s).view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(host(q), qo)
+
+
 def test_quantize_rejects_non_finite(reef):
     case("quantize non-finite -> NonFiniteInput")
     for bad in (math.nan, math.inf, -math.inf):
