@@ -193,6 +193,15 @@ __device__ __forceinline__ float scale_at(const float *s, int gran, int b, int h
     if (gran == REEF_SCALE_PER_HEAD) return s[h];
     return s[((int64_t)b * heads + h) * tokens + t];
 }
+// The same for a uniform (b, h) and token 0, as a scalar load (the scales are
+// read-only during a launch).
+__device__ __forceinline__ float scale_uni(const float *s, int gran, int b, int h, int heads,
+                                           int tokens) {
+    const int64_t i = gran == REEF_SCALE_PER_TENSOR ? 0
+                      : gran == REEF_SCALE_PER_HEAD ? h
+                                                    : ((int64_t)b * heads + h) * tokens;
+    return *(const __attribute__((address_space(4))) float *)(s + i);
+}
 
 // Scores relative to the row's running maximum s_run, read as floats without a
 // conversion: the integer product accumulates from the bit pattern 0x4B400000 - s_run,
@@ -335,8 +344,8 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
             qop[t] = row_ok ? *reinterpret_cast<const i32x4 *>(qrow + 32 * t + 16 * grp)
                             : i32x4{0, 0, 0, 0};
     }
-    const float ck = scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-    const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    const float ck = scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len);
+    const float cv = scale_uni(a.vs, a.kv_gran, b, kvh, a.kv_heads, a.kv_len);
     const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float c = cq * ck * a.score_scale;  // log2-domain score per unit of int32 sum
     const float kc = __builtin_fmaf(kBiasF, c, -kShift);
@@ -756,7 +765,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
 // schedules: 127 s_v, the largest magnitude the engine's quantize_int8 produces).
 __device__ __forceinline__ bool needs_lo(const PackedArgs &a, int b, int kvh) {
     if (a.all_precise) return true;
-    return 127.0f * scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) > kHiOnlyMax;
+    return 127.0f * scale_uni(a.vs, a.kv_gran, b, kvh, a.kv_heads, a.kv_len) > kHiOnlyMax;
 }
 
 // XCD y's share of the work: the (batch, head) pairs [bh0, bh0 + nh), an eighth of
@@ -835,8 +844,8 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(Pac
         // varies by row).
         const float c_item = a.q_gran == REEF_SCALE_PER_TOKEN
                                  ? INFINITY
-                                 : scale_at(a.qs, a.q_gran, b, h, 0, a.q_heads, a.q_len) *
-                                       scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) *
+                                 : scale_uni(a.qs, a.q_gran, b, h, a.q_heads, a.q_len) *
+                                       scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len) *
                                        a.score_scale;
         const bool fast = c_item <= kFastCMax;
         auto run = [&](auto lo_tag, auto fast_tag) {
@@ -908,8 +917,8 @@ __device__ void merge_parts(const PackedArgs &a, int b, int h, int tile, int par
     const int row = tile * kBM + wave * 32 + col;
     const bool row_ok = row < a.q_len;
     const int G = gridDim.x;
-    const float ck = scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
-    const float cv = scale_at(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len);
+    const float ck = scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len);
+    const float cv = scale_uni(a.vs, a.kv_gran, b, kvh, a.kv_heads, a.kv_len);
     const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float c = cq * ck * a.score_scale;
     auto get = [](const uint64_t *p) {
@@ -1020,8 +1029,8 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_bal_kernel
         const bool lo_p = needs_lo(a, b, kvh);
         const float c_item = a.q_gran == REEF_SCALE_PER_TOKEN
                                  ? INFINITY
-                                 : scale_at(a.qs, a.q_gran, b, h, 0, a.q_heads, a.q_len) *
-                                       scale_at(a.ks, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) *
+                                 : scale_uni(a.qs, a.q_gran, b, h, a.q_heads, a.q_len) *
+                                       scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len) *
                                        a.score_scale;
         const bool fast = c_item <= kFastCMax;
         if (lo_p) {
