@@ -585,21 +585,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64, PAGED ? kWgPerCu : 1) void decod
                 if (head_ok) {
 #pragma unroll
                     for (int d = 0; d < DB; ++d) {
-                        __hip_atomic_store(so + (2 * d) * kWave + lane, pack(o[d][0], o[d][1]),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(so + (2 * d + 1) * kWave + lane, pack(o[d][2], o[d][3]),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        part_store(so + (2 * d) * kWave + lane, pack(o[d][0], o[d][1]));
+                        part_store(so + (2 * d + 1) * kWave + lane, pack(o[d][2], o[d][3]));
                     }
-                    __hip_atomic_store(so + DecodeSlot<D>::O * kWave + lane, pack(m, l),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    part_store(so + DecodeSlot<D>::O * kWave + lane, pack(m, l));
                 }
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);
-                __builtin_amdgcn_s_waitcnt(0);  // vmcnt 0: every slot store has completed
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                part_stores_done();
                 uint32_t ticket = 0;
-                if (lane == 0)
-                    ticket = __hip_atomic_fetch_add(a.counters + item, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) ticket = part_count(a.counters + item);
                 ticket = __shfl(ticket, 0);
                 if (lane == 0) sLast = ticket == (uint32_t)(parts - 1) ? 1u : 0u;
             }
@@ -613,13 +606,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64, PAGED ? kWgPerCu : 1) void decod
             f32x4 op_run[DB];
 #pragma unroll
             for (int d = 0; d < DB; ++d) op_run[d] = f32x4{};
-            auto get = [](const uint64_t *q) {
-                return __hip_atomic_load(const_cast<uint64_t *>(q), __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            };
+            auto get = [](const uint64_t *q) { return part_load(q); };
             auto lo32 = [](uint64_t v) { return __uint_as_float((uint32_t)v); };
             auto hi32 = [](uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); };
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            part_claimed();
             if (head_ok) {
                 for (int gg = gf + wave; gg <= gl; gg += kDecodeWaves) {
                     if (wg_start(gg, T, G) == wg_start(gg + 1, T, G)) continue;  // empty
@@ -649,9 +639,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, PAGED ? kWgPerCu : 1) void decod
             }
             merge_waves<D>(mp_run, lp_run, op_run, sO, sML, wave, lane);
             if (wave == 0) {
-                if (lane == 0)
-                    __hip_atomic_store(a.counters + item, 0u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) part_reset(a.counters + item);
                 if (head_ok) {
                     const float inv = lp_run > 0.0f ? 1.0f / lp_run : 0.0f;
                     float *orow = out + ((int64_t)b * a.q_heads + head) * D;

@@ -640,13 +640,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
         auto pack = [](float x, float y) {
             return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
         };
-        auto put = [](uint64_t *p, uint64_t v) {
-            __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        };
-        auto get = [](const uint64_t *p) {
-            return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-        };
+        auto put = [](uint64_t *p, uint64_t v) { part_store(p, v); };
+        auto get = [](const uint64_t *p) { return part_load(p); };
         // Element e of wave w, lane l at [(w E + e) 64 + l]: each store is 512
         // contiguous bytes.
         uint64_t *so = reinterpret_cast<uint64_t *>(sa.slots + (int64_t)sp.slot * SF);
@@ -657,18 +652,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                 put(so + (wave * E + d * 8 + e) * kWave + lane,
                     pack(acc[d][2 * e], acc[d][2 * e + 1]));
         put(so + OF / 2 + wave * kWave + lane, pack(m_run, l_tot));
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);  // vmcnt 0: every slot store has completed
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        part_stores_done();
         __syncthreads();
-        if (tid == 0)
-            *sTicket = __hip_atomic_fetch_add(sa.counters + sp.item, 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) *sTicket = part_count(sa.counters + sp.item);
         __syncthreads();
         if (*sTicket != (uint32_t)(sp.parts - 1)) return;
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (tid == 0)  // ready for the next launch
-            __hip_atomic_store(sa.counters + sp.item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        part_claimed();
+        if (tid == 0) part_reset(sa.counters + sp.item);  // ready for the next launch
         // Parts in order: part p is workgroup first_wg + p; the first part sits in
         // its workgroup's second slot when that range began before the item.
         auto slot_of = [&](int p) {

@@ -727,10 +727,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
         // (written through beneath the per-XCD L2s) that complete before the barrier
         // below. The merge reads them the same way.
         uint64_t *so = a.slots + (int64_t)slot * kSlotWords;
-        auto put = [&](int e, uint64_t v) {
-            __hip_atomic_store(so + (wave * 33 + e) * 64 + lane, v, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        };
+        auto put = [&](int e, uint64_t v) { part_store(so + (wave * 33 + e) * 64 + lane, v); };
         auto pack2 = [](float x, float y) {
             return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
         };
@@ -739,9 +736,7 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
 #pragma unroll
             for (int e = 0; e < 8; ++e) put(8 * d + e, pack2(acc[d][2 * e], acc[d][2 * e + 1]));
         put(32, (uint64_t)(uint32_t)s_run | ((uint64_t)__float_as_uint(l_row) << 32));
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);  // every slot store has completed
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        part_stores_done();
     } else if (row_ok) {
         float *orow = a.out + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_st;
         const float norm = cv / l_row;
@@ -921,10 +916,7 @@ __device__ void merge_parts(const PackedArgs &a, int b, int h, int tile, int par
     const float cv = scale_uni(a.vs, a.kv_gran, b, kvh, a.kv_heads, a.kv_len);
     const float cq = row_ok ? scale_at(a.qs, a.q_gran, b, h, row, a.q_heads, a.q_len) : 0.0f;
     const float c = cq * ck * a.score_scale;
-    auto get = [](const uint64_t *p) {
-        return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-    };
+    auto get = [](const uint64_t *p) { return part_load(p); };
     // Part p is logical workgroup first_wg + p; the first part sits in that
     // workgroup's second slot when its range began before this tile.
     auto slot_of = [&](int p) {
@@ -1042,15 +1034,12 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_bal_kernel
         }
         if (parts > 1) {
             // The tile call ended with a barrier after every slot store completed.
-            if (threadIdx.x == 0)
-                sTicket = __hip_atomic_fetch_add(ba.counters + (int64_t)bh * a.q_tiles + tile, 1u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t *counter = ba.counters + (int64_t)bh * a.q_tiles + tile;
+            if (threadIdx.x == 0) sTicket = part_count(counter);
             __syncthreads();
             if (sTicket == (uint32_t)(parts - 1)) {
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);
-                if (threadIdx.x == 0)  // ready for the next launch
-                    __hip_atomic_store(ba.counters + (int64_t)bh * a.q_tiles + tile, 0u,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                part_claimed();
+                if (threadIdx.x == 0) part_reset(counter);  // ready for the next launch
                 merge_parts(a, b, h, tile, parts, first_wg, item_u0, ba.units);
             }
         }

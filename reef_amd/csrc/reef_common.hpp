@@ -105,6 +105,50 @@ __device__ __forceinline__ void flag_status(uint32_t *word, uint32_t bits) {
     if (word) atomicOr(word, bits);
 }
 
+// --- cross-workgroup parts (decode and prefill merges) -----------------------------------
+//
+// A result cut across workgroups is merged by the part that counts in last:
+//   publish: every thread stores its part with part_store, then part_stores_done();
+//   a barrier; one thread counts the part in with part_count (the old count);
+//   claim: the part whose count was parts - 1 reads every part with part_load (after
+//   its count returned) and resets the counter with part_reset.
+// The ordering rests on the gfx950 memory model as LLVM implements it (AMDGPUUsage,
+// "Memory Model GFX942", which gfx950 follows), not on release/acquire: monotonic
+// atomic loads, stores and read-modify-writes at agent scope compile to global or flat
+// accesses with sc1 set, which bypass the per-XCD L2 and are coherent at the memory
+// side; s_waitcnt vmcnt(0) returns only when every earlier store has completed there;
+// the signal fences keep the compiler from moving memory accesses across that wait.
+// A release/acquire pair would order the same accesses under the language model,
+// but compiles to an L2 write-back (buffer_wbl2) and invalidate (buffer_inv) of the
+// whole XCD on every cut item, which the other workgroups then pay in misses.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the cross-workgroup part protocol is written for gfx950"
+#endif
+
+__device__ __forceinline__ void part_store(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t part_load(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every part_store of this thread has completed before any later access is issued.
+__device__ __forceinline__ void part_stores_done() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Counts a part in; the previous count (parts - 1: this part merges). The caller
+// places part_claimed() after reading the result, before its first part_load.
+__device__ __forceinline__ uint32_t part_count(uint32_t *counter) {
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void part_claimed() { __atomic_signal_fence(__ATOMIC_SEQ_CST); }
+// Leaves the counter at zero for the next launch (after the last count of this item).
+__device__ __forceinline__ void part_reset(uint32_t *counter) {
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // --- host helpers -----------------------------------------------------------------------
 
 inline bool aligned(const void *p, size_t bytes) {
