@@ -67,7 +67,7 @@ constexpr int kQueueWords = kXcdCount + 1;
 struct PartInfo {
     int32_t c0, c1, slot, pad;
 };
-constexpr int kSmem = kKRing + kVRing + (int)sizeof(PartInfo);
+constexpr int kSmem = kKRing + kVRing + 2 * (int)sizeof(PartInfo);  // part, queue state
 // A part slot (8-byte words): per wave and lane, the 64 accumulators in register
 // order, then (running maximum, row sum); word e of wave w, lane l at [(w E + e) 64 + l].
 constexpr int kSlotWords = kWaves * 33 * 64;
@@ -302,12 +302,9 @@ __device__ __forceinline__ void keep(const T &x) {
     asm volatile("" ::"v"(x));
 }
 
-template <bool LO, bool FAST, bool TAP = false>
-__device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, int b_in, int h_in,
-                                                      int tile_in, int8_t *smem_in) {
-    const PackedArgs a = uniform_args(args);
-    const int b = uni(b_in), h = uni(h_in), tile = uni(tile_in);
-    lds_i8 *const smem = (lds_i8 *)uni(smem_in);
+template <bool LO, bool FAST, bool TAP>
+__device__ __forceinline__ void tile_body(const PackedArgs &a, const int b, const int h,
+                                          const int tile, lds_i8 *const smem) {
     constexpr int DB = kPD / 32;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -755,6 +752,13 @@ __device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, in
     __syncthreads();
 }
 
+template <bool LO, bool FAST>
+__device__ __attribute__((noinline)) void packed_tile(const PackedArgs &args, int b_in, int h_in,
+                                                      int tile_in, int8_t *smem_in) {
+    tile_body<LO, FAST, false>(uniform_args(args), uni(b_in), uni(h_in), uni(tile_in),
+                               (lds_i8 *)uni(smem_in));
+}
+
 // Whether P needs hi + lo parts for (batch, kv head): its value scale allows
 // dequantized magnitudes above kHiOnlyMax (the same rule as the other prefill
 // schedules: 127 s_v, the largest magnitude the engine's quantize_int8 produces).
@@ -782,82 +786,134 @@ __device__ __forceinline__ Share share_of(const PackedArgs &a, int y) {
     return s;
 }
 
+// The queue state of a workgroup, in LDS after the part record: the unit taken last
+// (its XCD share and index, or unit -1 when every queue is empty) and the number of
+// queues found empty so far (the own XCD's first).
+struct QueueState {
+    int32_t share, unit, tried, pad;
+};
+constexpr int kQueueOff = kKRing + kVRing + (int)sizeof(PartInfo);
+static_assert(kQueueOff + (int)sizeof(QueueState) <= kSmem, "queue state in LDS");
+
+// Thread 0: takes the next unit into q (unit -1 when every queue is empty). The caller
+// places a barrier before the unit is read.
+__device__ __forceinline__ void take_unit(const PackedArgs &a,
+                                          __attribute__((address_space(3))) QueueState *q) {
+    const int x = blockIdx.x % kXcdCount;
+    int tried = q->tried;
+    int unit = -1, share = 0;
+    while (tried < kXcdCount) {
+        share = (x + tried) % kXcdCount;
+        const uint32_t n = __hip_atomic_fetch_add(a.queue + share, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        if ((int64_t)n < share_of(a, share).units) {
+            unit = (int)n;
+            break;
+        }
+        ++tried;
+    }
+    q->tried = tried;
+    q->share = share;
+    q->unit = unit;
+}
+
+// (batch x head, light tile, heavy tile or -1) of unit u of XCD share y.
+struct Unit {
+    int bh, first, second;
+};
+__device__ __forceinline__ Unit unit_tiles(const PackedArgs &a, int y, int u) {
+    const Share s = share_of(a, y);
+    Unit r;
+    r.second = -1;
+    if (u < s.pairs) {
+        r.bh = s.bh0 + u / a.per_head;
+        r.first = u % a.per_head;                  // the light tile, whose keys are a prefix
+        if (a.q_tiles - 1 - r.first != r.first) r.second = a.q_tiles - 1 - r.first;  // of the heavy's
+    } else {
+        const int v = u - s.pairs;
+        r.bh = s.bh0 + (s.nh - s.tail) + v % s.tail;
+        r.first = a.q_tiles - 1 - v / s.tail;
+    }
+    return r;
+}
+
+// The tile-function variant of (batch, head): bit 0 hi + lo P, bit 1 one FMA per
+// probability (the score factor c small enough that 12582912 c rounds within 1/4;
+// not with per-token q scales, where c varies by row).
+__device__ __forceinline__ int head_variant(const PackedArgs &a, int b, int h) {
+    const int kvh = h / (a.q_heads / a.kv_heads);
+    const float c = a.q_gran == REEF_SCALE_PER_TOKEN
+                        ? INFINITY
+                        : scale_uni(a.qs, a.q_gran, b, h, a.q_heads, a.q_len) *
+                              scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len) *
+                              a.score_scale;
+    return (needs_lo(a, b, kvh) ? 1 : 0) | (c <= kFastCMax ? 2 : 0);
+}
+
+// Units of one variant, from the unit in the queue state on: computes each unit's
+// tiles and takes the next unit, until every queue is empty (returns -1) or the next
+// unit needs another variant (returns that variant; the unit stays in the queue state
+// for the next call). One call per workgroup and variant: the launch arguments,
+// scales and registers of a call are set up once, not per tile.
+template <bool LO, bool FAST, bool TAP>
+__device__ __attribute__((noinline)) int packed_units(const PackedArgs &args, int8_t *smem_in) {
+    const PackedArgs a = uniform_args(args);
+    lds_i8 *const smem = (lds_i8 *)uni(smem_in);
+    auto *q = (__attribute__((address_space(3))) QueueState *)(smem + kQueueOff);
+    constexpr int kMine = (LO ? 1 : 0) | (FAST ? 2 : 0);
+    for (;;) {
+        const int y = uni(q->share), u = uni(q->unit);
+        if (u < 0) return -1;
+        const Unit t = unit_tiles(a, y, u);
+        const int b = t.bh / a.q_heads, h = t.bh % a.q_heads;
+        if (!TAP) {
+            const int var = head_variant(a, b, h);
+            if (var != kMine) return var;
+        }
+        tile_body<LO, FAST, TAP>(a, b, h, t.first, smem);
+        if (t.second >= 0) tile_body<LO, FAST, TAP>(a, b, h, t.second, smem);
+        // The tile body ended with a barrier: every thread has read the queue state.
+        if (threadIdx.x == 0) take_unit(a, q);
+        __syncthreads();
+    }
+}
+
 // Two workgroups per compute unit: the two waves on each SIMD belong to different
 // workgroups and fill each other's waits. Units are taken from a queue per XCD (its
 // share above, in order, as the workgroups finish the previous one), then from the
-// other XCDs' queues. Units differ in cost (the hi + lo products of a head's precise
-// value blocks, and the single tiles): with pairs dealt out in a fixed order the
-// last workgroups ended 15 % after the mean (4x32x8192x128: 2.30 ms dealt out,
-// 2.18-2.19 ms from the queues of pairs, whose last workgroups still ended 7 %
-// after the mean; with the single tiles last 3 %, 1 % faster; with four single
-// tiles per workgroup instead of two, 2173 against 2213 us over six runs on one
-// box, and no run slower than 2.2 ms). The last workgroup to finish resets the
-// queue to zero for the next call.
+// other XCDs' queues. Units differ in cost (the single tiles; heads with hi + lo P):
+// with pairs dealt out in a fixed order the last workgroups ended 15 % after the mean
+// (4x32x8192x128: 2.30 ms dealt out, 2.18-2.19 ms from the queues of pairs, whose
+// last workgroups still ended 7 % after the mean; with the single tiles last 3 %, 1 %
+// faster; with four single tiles per workgroup instead of two, 2173 against 2213 us
+// over six runs on one box, and no run slower than 2.2 ms). The last workgroup to
+// finish resets the queue to zero for the next call.
 __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_kernel(PackedArgs a) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[kSmem];
-    __shared__ int sUnit[2];  // XCD share and unit, or -1
-    const int x = blockIdx.x % kXcdCount;
-    if (threadIdx.x == 0)  // every call computes a whole query tile (ordered by the first barrier)
+    auto *q = reinterpret_cast<QueueState *>(smem + kQueueOff);
+    if (threadIdx.x == 0) {
+        // Every call computes a whole query tile.
         *reinterpret_cast<PartInfo *>(smem + kKRing + kVRing) = PartInfo{0, INT32_MAX, -1, 0};
-    int tried = 0;  // queues found empty, own XCD's first
-    auto take = [&](int &share) -> int {  // thread 0: the next unit, or -1 when all are taken
-        while (tried < kXcdCount) {
-            share = (x + tried) % kXcdCount;
-            const uint32_t n = __hip_atomic_fetch_add(a.queue + share, 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-            if ((int64_t)n < share_of(a, share).units) return (int)n;
-            ++tried;
-        }
-        return -1;
-    };
+        q->tried = 0;
+        take_unit(a, (__attribute__((address_space(3))) QueueState *)q);
+    }
+    __syncthreads();
     for (;;) {
-        if (threadIdx.x == 0) {
-            int share = 0;
-            sUnit[1] = take(share);
-            sUnit[0] = share;
-        }
-        __syncthreads();
-        const int y = sUnit[0], u = sUnit[1];
-        __syncthreads();  // every thread has read sUnit before thread 0 writes it again
+        const int u = __builtin_amdgcn_readfirstlane(q->unit);
         if (u < 0) break;
-        const Share s = share_of(a, y);
-        int bh, first, second = -1;
-        if (u < s.pairs) {
-            bh = s.bh0 + u / a.per_head;
-            first = u % a.per_head;                 // the light tile, whose keys are a prefix
-            if (a.q_tiles - 1 - first != first) second = a.q_tiles - 1 - first;  // of the heavy's
-        } else {
-            const int v = u - s.pairs;
-            bh = s.bh0 + (s.nh - s.tail) + v % s.tail;
-            first = a.q_tiles - 1 - v / s.tail;
-        }
-        const int b = bh / a.q_heads, h = bh % a.q_heads;
-        const int kvh = h / (a.q_heads / a.kv_heads);
-        const bool lo = needs_lo(a, b, kvh);
-        // One FMA per probability when the score factor c is small enough that
-        // 12582912 c rounds within 1/4 (any q scale granularity but per token, where c
-        // varies by row).
-        const float c_item = a.q_gran == REEF_SCALE_PER_TOKEN
-                                 ? INFINITY
-                                 : scale_uni(a.qs, a.q_gran, b, h, a.q_heads, a.q_len) *
-                                       scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len) *
-                                       a.score_scale;
-        const bool fast = c_item <= kFastCMax;
-        auto run = [&](auto lo_tag, auto fast_tag) {
-            constexpr bool LO = decltype(lo_tag)::value, FAST = decltype(fast_tag)::value;
-            packed_tile<LO, FAST>(a, b, h, first, smem);
-            if (second >= 0) packed_tile<LO, FAST>(a, b, h, second, smem);
-        };
+        int var;
         if (a.tap) {  // the score hook's launch: one fp16 P, small c (see the entry point)
-            packed_tile<false, true, true>(a, b, h, first, smem);
-            if (second >= 0) packed_tile<false, true, true>(a, b, h, second, smem);
-        } else if (lo) {
-            if (fast) run(std::true_type{}, std::true_type{});
-            else run(std::true_type{}, std::false_type{});
+            var = packed_units<false, true, true>(a, smem);
         } else {
-            if (fast) run(std::false_type{}, std::true_type{});
-            else run(std::false_type{}, std::false_type{});
+            const Unit t = unit_tiles(a, __builtin_amdgcn_readfirstlane(q->share), u);
+            switch (head_variant(a, t.bh / a.q_heads, t.bh % a.q_heads)) {
+            case 0: var = packed_units<false, false, false>(a, smem); break;
+            case 1: var = packed_units<true, false, false>(a, smem); break;
+            case 2: var = packed_units<false, true, false>(a, smem); break;
+            default: var = packed_units<true, true, false>(a, smem); break;
+            }
         }
+        if (__builtin_amdgcn_readfirstlane(var) < 0) break;
     }
     // Every take of this workgroup has returned; the last workgroup to count itself
     // here is the last to use the queue.
@@ -1018,19 +1074,11 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_bal_kernel
         if (threadIdx.x == 0)
             *sPart = PartInfo{c0, c1, parts > 1 ? 2 * L + (first ? 0 : 1) : -1, 0};
         __syncthreads();
-        const bool lo_p = needs_lo(a, b, kvh);
-        const float c_item = a.q_gran == REEF_SCALE_PER_TOKEN
-                                 ? INFINITY
-                                 : scale_uni(a.qs, a.q_gran, b, h, a.q_heads, a.q_len) *
-                                       scale_uni(a.ks, a.kv_gran, b, kvh, a.kv_heads, a.kv_len) *
-                                       a.score_scale;
-        const bool fast = c_item <= kFastCMax;
-        if (lo_p) {
-            if (fast) packed_tile<true, true>(a, b, h, tile, smem);
-            else packed_tile<true, false>(a, b, h, tile, smem);
-        } else {
-            if (fast) packed_tile<false, true>(a, b, h, tile, smem);
-            else packed_tile<false, false>(a, b, h, tile, smem);
+        switch (head_variant(a, b, h)) {
+        case 0: packed_tile<false, false>(a, b, h, tile, smem); break;
+        case 1: packed_tile<true, false>(a, b, h, tile, smem); break;
+        case 2: packed_tile<false, true>(a, b, h, tile, smem); break;
+        default: packed_tile<true, true>(a, b, h, tile, smem); break;
         }
         if (parts > 1) {
             // The tile call ended with a barrier after every slot store completed.
