@@ -47,10 +47,13 @@ struct PrefillArgs {
     int32_t q_gran, kv_gran;
     int32_t q_tiles;
     int32_t zigzag;  // pair heavy and light tiles in grids that fit at once
-    // Items this launch computes (per-tensor / per-head K/V scales): 0 all, 1 those
-    // whose largest dequantized value 127 s_v is at most kHiOnlyMax, 2 the others.
-    int32_t item_sel;
 };
+
+// Precision of P in a launch: hi + lo parts everywhere, or the choice per item (hi + lo
+// where the item's values reach above kHiOnlyMax, else one fp16 P). One launch holds
+// both bodies, at the hi + lo body's occupancy (one workgroup per SIMD set), rather
+// than one launch per choice, which costs about 5 us where it finds no item.
+constexpr int kPrecHiLo = 1, kPrecPerItem = 2;
 
 // Balanced schedule: the steps (item, key tile) of all items, items in (batch,
 // head, query tile) order and each item's tiles in key order, are cut into G
@@ -740,7 +743,7 @@ __device__ __forceinline__ bool item_is_wide(const PrefillArgs &a, int b, int h)
 // reverse order, so that with heaviest-first ranks every workgroup's sum of work
 // is about the same. A workgroup's next item starts while the stores of its last
 // one drain.
-template <int D, bool PRECISE>
+template <int D, int PREC>
 __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillArgs a, int items) {
     static_assert(4 * (D / 32) * 4 * kWave * 16 + 4 * kWave * 8 <= 2 * PrefillLds<D>::BYTES,
                   "merge buffer fits in the stages");
@@ -755,30 +758,36 @@ __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillA
         }
         int tile, b, h;
         item_coords(a, item, tile, b, h);
-        if (a.item_sel != 0 && item_is_wide(a, b, h) != (a.item_sel == 2)) continue;  // uniform
-        prefill_body<D, false, PRECISE, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
-                                                StreamPart{}, nullptr);
+        if (PREC == kPrecHiLo || (PREC == kPrecPerItem && item_is_wide(a, b, h)))  // uniform
+            prefill_body<D, false, true, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
+                                                 StreamPart{}, nullptr);
+        else
+            prefill_body<D, false, false, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
+                                                  StreamPart{}, nullptr);
         __syncthreads();  // the next item's stages overwrite the merge buffer
     }
 }
 
-template <int D, bool KV_TOKEN, bool PRECISE>
-__global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_kernel(PrefillArgs a) {
+template <int D, bool KV_TOKEN, int PREC>
+__global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
     int tile, b, h;
     item_coords(a, grid_rank(a), tile, b, h);
-    if (!KV_TOKEN && a.item_sel != 0 && item_is_wide(a, b, h) != (a.item_sel == 2)) return;
-    prefill_body<D, KV_TOKEN, PRECISE, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
-                                               StreamArgs{}, StreamPart{}, nullptr);
+    if (KV_TOKEN || PREC == kPrecHiLo || (PREC == kPrecPerItem && item_is_wide(a, b, h)))
+        prefill_body<D, KV_TOKEN, true, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
+                                                StreamArgs{}, StreamPart{}, nullptr);
+    else
+        prefill_body<D, KV_TOKEN, false, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
+                                                 StreamArgs{}, StreamPart{}, nullptr);
 }
 
 // Balanced schedule (StreamArgs): workgroup g works through the steps
 // [L G^-1 units, (L + 1) G^-1 units) of logical workgroup L, where the G / 8
 // workgroups that run on one XCD (hardware workgroup g goes to XCD g % 8) hold
 // consecutive L, so an XCD's L2 sees a few heads, not all of them.
-template <int D, bool KV_TOKEN, bool PRECISE>
-__global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefill_stream_kernel(
+template <int D, bool KV_TOKEN, int PREC>
+__global__ __launch_bounds__(kThreads, 1) void prefill_stream_kernel(
     PrefillArgs a, StreamArgs sa) {
     __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
@@ -815,12 +824,14 @@ __global__ __launch_bounds__(kThreads, (KV_TOKEN || PRECISE) ? 1 : 2) void prefi
         sp.parts = wg_of(sp.item_u0 + n - 1) - sp.first_wg + 1;
         sp.slot = 2 * L + (first ? 0 : 1);
         sp.item = bh * a.q_tiles + tile;
-        // With item_sel, one launch takes the items whose values need hi + lo P and
-        // another the rest; each walks the same ranges and skips the other's items.
-        if (KV_TOKEN || a.item_sel == 0 ||
-            item_is_wide(a, bh / a.q_heads, bh % a.q_heads) == (a.item_sel == 2))
-            prefill_body<D, KV_TOKEN, PRECISE, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads,
-                                                        c0, c1, smem, sScale, sa, sp, &sTicket);
+        // Every part of an item takes the same precision (a function of the item).
+        if (KV_TOKEN || PREC == kPrecHiLo ||
+            (PREC == kPrecPerItem && item_is_wide(a, bh / a.q_heads, bh % a.q_heads)))
+            prefill_body<D, KV_TOKEN, true, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0,
+                                                     c1, smem, sScale, sa, sp, &sTicket);
+        else
+            prefill_body<D, KV_TOKEN, false, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0,
+                                                      c1, smem, sScale, sa, sp, &sTicket);
         u += c1 - c0;
         c0 = 0;
         first = false;
@@ -894,7 +905,8 @@ int64_t host_steps_before(const reef_attention_params &p, int64_t t) {
     return s;
 }
 
-// The balanced schedule's grid: two 4-wave workgroups per compute unit.
+// Bound on the balanced schedule's grid (two part slots per workgroup are sized for
+// it): two 4-wave workgroups per compute unit.
 int64_t stream_groups() { return 2 * compute_units(); }
 
 // The balanced schedule's workspace layout is the same for every call: a fixed
@@ -1081,7 +1093,6 @@ extern "C" reef_status reef_attention_prefill_int8(
     // split is the only parallelism left to balance the causal work.
     if (sched == REEF_ATTN_SCHED_BALANCED && !stream_ok) return REEF_INVALID_ARGUMENT;
     if (sched == REEF_ATTN_SCHED_SPLIT && tok) return REEF_INVALID_ARGUMENT;
-    a.item_sel = 0;
     if (sched == REEF_ATTN_SCHED_BALANCED ||
         (sched == REEF_ATTN_SCHED_AUTO && stream_ok &&
          (precise ? items < compute_units() : items <= compute_units()))) {
@@ -1095,39 +1106,29 @@ extern "C" reef_status reef_attention_prefill_int8(
         if (sa.units >= (int64_t(1) << 40)) return REEF_UNSUPPORTED;
         // No more workgroups than steps: every range holds at least one step, so the
         // workgroups between an item's first and last part each hold a part of it.
-        // The precise kernels hold a compute unit alone: at most one workgroup per
-        // unit, so that every workgroup runs at once, and at least kStreamMinSteps
-        // steps per workgroup, so that a short chunk of queries over a long prefix is
-        // cut into a few parts per item (each merge reads its parts one after another).
-        auto grid_of = [&](bool prec) {
-            const int64_t groups =
-                prec ? std::max<int64_t>(1, std::min<int64_t>(compute_units(),
-                                                              sa.units / kStreamMinSteps))
-                     : stream_groups();
-            return dim3((unsigned)std::min<int64_t>(groups, sa.units));
-        };
-#define REEF_STREAM_LAUNCH(DIM, TOK, PREC)                                                   \
-    hipLaunchKernelGGL((prefill_stream_kernel<DIM, TOK, PREC>), grid_of(PREC), dim3(kThreads), \
-                       0, stream, a, sa)
-        if (precise) {
-            if (D == 128) {
-                if (tok) REEF_STREAM_LAUNCH(128, true, true);
-                else REEF_STREAM_LAUNCH(128, false, true);
-            } else {
-                if (tok) REEF_STREAM_LAUNCH(64, true, true);
-                else REEF_STREAM_LAUNCH(64, false, true);
-            }
-            return launch_status();
+        // A workgroup holds a compute unit alone: at most one workgroup per unit, so
+        // that every workgroup runs at once, and at least kStreamMinSteps steps per
+        // workgroup, so that a short chunk of queries over a long prefix is cut into a
+        // few parts per item (each merge reads its parts one after another).
+        const dim3 sgrid((unsigned)std::min<int64_t>(
+            std::max<int64_t>(1, std::min<int64_t>(compute_units(), sa.units / kStreamMinSteps)),
+            sa.units));
+#define REEF_STREAM_LAUNCH(DIM, TOK, PREC)                                                 \
+    hipLaunchKernelGGL((prefill_stream_kernel<DIM, TOK, PREC>), sgrid, dim3(kThreads), 0, \
+                       stream, a, sa)
+        // One launch: hi + lo P everywhere (the precision flag, per-token K/V scales)
+        // or per item, on the precise kernels' grid (items whose values stay within
+        // kHiOnlyMax, which take one fp16 P, are rare in practice).
+        if (tok) {
+            if (D == 128) REEF_STREAM_LAUNCH(128, true, kPrecHiLo);
+            else REEF_STREAM_LAUNCH(64, true, kPrecHiLo);
+        } else if (precise) {
+            if (D == 128) REEF_STREAM_LAUNCH(128, false, kPrecHiLo);
+            else REEF_STREAM_LAUNCH(64, false, kPrecHiLo);
+        } else {
+            if (D == 128) REEF_STREAM_LAUNCH(128, false, kPrecPerItem);
+            else REEF_STREAM_LAUNCH(64, false, kPrecPerItem);
         }
-        // Items whose values stay within kHiOnlyMax take one fp16 P, the others the
-        // hi + lo split (the precise kernel's grid); each launch skips the other's items.
-        a.item_sel = 1;
-        if (D == 128) REEF_STREAM_LAUNCH(128, false, false);
-        else REEF_STREAM_LAUNCH(64, false, false);
-        if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
-        a.item_sel = 2;
-        if (D == 128) REEF_STREAM_LAUNCH(128, false, true);
-        else REEF_STREAM_LAUNCH(64, false, true);
 #undef REEF_STREAM_LAUNCH
         return launch_status();
     }
@@ -1143,43 +1144,27 @@ extern "C" reef_status reef_attention_prefill_int8(
     hipLaunchKernelGGL((prefill_split_kernel<DIM, PREC>), pgrid, dim3(2 * kThreads), 0, stream, a, \
                        (int)items)
         if (precise) {
-            if (D == 128) REEF_SPLIT_LAUNCH(128, true);
-            else REEF_SPLIT_LAUNCH(64, true);
-            return launch_status();
+            if (D == 128) REEF_SPLIT_LAUNCH(128, kPrecHiLo);
+            else REEF_SPLIT_LAUNCH(64, kPrecHiLo);
+        } else {  // one fp16 P or hi + lo per item, in one launch
+            if (D == 128) REEF_SPLIT_LAUNCH(128, kPrecPerItem);
+            else REEF_SPLIT_LAUNCH(64, kPrecPerItem);
         }
-        // Items whose values stay within kHiOnlyMax take one fp16 P, the others the
-        // hi + lo split; each launch skips the other's items.
-        a.item_sel = 1;
-        if (D == 128) REEF_SPLIT_LAUNCH(128, false);
-        else REEF_SPLIT_LAUNCH(64, false);
-        if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
-        a.item_sel = 2;
-        if (D == 128) REEF_SPLIT_LAUNCH(128, true);
-        else REEF_SPLIT_LAUNCH(64, true);
 #undef REEF_SPLIT_LAUNCH
         return launch_status();
     }
 #define REEF_PREFILL_LAUNCH(DIM, TOK, PREC)                                                  \
     hipLaunchKernelGGL((prefill_kernel<DIM, TOK, PREC>), grid, dim3(kThreads), 0, stream, a)
-    if (tok || precise) {  // per-token K/V scales always split P
-        if (D == 128) {
-            if (tok) REEF_PREFILL_LAUNCH(128, true, true);
-            else REEF_PREFILL_LAUNCH(128, false, true);
-        } else {
-            if (tok) REEF_PREFILL_LAUNCH(64, true, true);
-            else REEF_PREFILL_LAUNCH(64, false, true);
-        }
-        return launch_status();
+    if (tok) {  // per-token K/V scales always split P
+        if (D == 128) REEF_PREFILL_LAUNCH(128, true, kPrecHiLo);
+        else REEF_PREFILL_LAUNCH(64, true, kPrecHiLo);
+    } else if (precise) {
+        if (D == 128) REEF_PREFILL_LAUNCH(128, false, kPrecHiLo);
+        else REEF_PREFILL_LAUNCH(64, false, kPrecHiLo);
+    } else {  // one fp16 P or hi + lo per item, in one launch
+        if (D == 128) REEF_PREFILL_LAUNCH(128, false, kPrecPerItem);
+        else REEF_PREFILL_LAUNCH(64, false, kPrecPerItem);
     }
-    // Items whose values stay within kHiOnlyMax take one fp16 P, the others the
-    // hi + lo split; each launch returns at once from the other's items.
-    a.item_sel = 1;
-    if (D == 128) REEF_PREFILL_LAUNCH(128, false, false);
-    else REEF_PREFILL_LAUNCH(64, false, false);
-    if (hipGetLastError() != hipSuccess) return REEF_HIP_ERROR;
-    a.item_sel = 2;
-    if (D == 128) REEF_PREFILL_LAUNCH(128, false, true);
-    else REEF_PREFILL_LAUNCH(64, false, true);
 #undef REEF_PREFILL_LAUNCH
     return launch_status();
 }
