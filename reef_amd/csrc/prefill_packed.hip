@@ -1070,7 +1070,6 @@ __global__ __launch_bounds__(64 * kWaves, kPerCu) void prefill_packed_bal_kernel
         const int first_wg = wg_of(item_u0);
         const int parts = wg_of(item_u0 + n - 1) - first_wg + 1;
         const int b = bh / a.q_heads, h = bh % a.q_heads;
-        const int kvh = h / (a.q_heads / a.kv_heads);
         if (threadIdx.x == 0)
             *sPart = PartInfo{c0, c1, parts > 1 ? 2 * L + (first ? 0 : 1) : -1, 0};
         __syncthreads();
