@@ -199,15 +199,16 @@ def prefill_kernels(torch, cfg):
     or per-head scales, a workspace): the packed schedule (a V-image pack, then the
     attention kernel) when head_dim is 128 and there is at least one pair of 256-row
     query tiles per compute unit; the balanced schedule with at most one 128-row
-    query tile per compute unit (one launch for the items with one fp16 P, one for
-    those that need hi + lo P); the one-item kernel otherwise."""
+    query tile per compute unit; otherwise the split kernel at head_dim 128 and the
+    one-item kernel at 64. Each is one launch, which splits P into fp16 hi + lo parts
+    for the items whose values need it."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     pairs = ((cfg.seq + 255) // 256 + 1) // 2 * cfg.batch * cfg.q_heads
     if cfg.head_dim == 128 and pairs >= cus:
         return "vt_pack_kernel + prefill_packed_kernel"
     if (cfg.seq + 127) // 128 * cfg.batch * cfg.q_heads <= cus:
-        return "prefill_stream_kernel (fp16 P + hi/lo P launches)"
-    return "prefill_kernel"
+        return "prefill_stream_kernel"
+    return "prefill_split_kernel" if cfg.head_dim == 128 else "prefill_kernel"
 
 
 def bench_prefill(torch, reef, W, name, steps, warmup, with_quant=True):

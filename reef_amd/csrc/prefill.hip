@@ -1039,12 +1039,6 @@ extern "C" reef_status reef_attention_prefill_int8(
     // fp16 rounding, which no longer cancels against the row sum; those launches
     // always split P into fp16 hi + lo parts to stay well inside the tolerance.
     const bool precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0 || tok;
-    // With no more items than compute units, the key split of the persistent
-    // kernel is the only parallelism left to balance the causal work; with more,
-    // two one-item workgroups per compute unit overlap each other's prologue and
-    // epilogue better.
-    // The balanced schedule needs the caller's workspace; without it, small grids
-    // take the persistent split kernel.
     if (workspace && !aligned(workspace, 256)) return REEF_INVALID_ARGUMENT;
     const uint32_t sched = p->flags & REEF_ATTN_SCHED_MASK;
     if (sched != REEF_ATTN_SCHED_AUTO && sched != REEF_ATTN_SCHED_ONE_ITEM &&
@@ -1082,20 +1076,22 @@ extern "C" reef_status reef_attention_prefill_int8(
                                      ost, static_cast<char *>(workspace) + bal_bytes, work, stream);
     }
     // Every schedule splits P into hi + lo where the values need it: always with the
-    // precision flag or per-token K/V scales, otherwise per item (two launches, each
-    // skipping the other's items). The library takes the balanced schedule, which
-    // cuts the causal work of all items into equal ranges, for grids of at most one
-    // 128-row tile per compute unit (1x8q/1kv x4096x128: 54 against 70 us with the
-    // split kernel and 82 us with the one-item kernel; with precision, fewer tiles
-    // than units: a short chunk of queries over a long cache); with more tiles, two
-    // one-item workgroups per compute unit do as well (1x32x2048x128: 54 against 57
-    // us balanced). Without a workspace small grids take the split kernel, whose key
-    // split is the only parallelism left to balance the causal work.
+    // precision flag or per-token K/V scales, otherwise per item, in one launch. The
+    // library takes the balanced schedule, which cuts the causal work of all items
+    // into equal ranges, for grids of at most one 128-row tile per compute unit
+    // (1x8q/1kv x4096x128: 71 us against 86 us with the split kernel and 101 us with
+    // the one-item kernel; 69 against 84 and 97 us with the precision flag). On
+    // larger grids, head_dim 128 takes the split kernel, whose two 4-wave groups per
+    // workgroup halve each tile's key loop (1x32x2048x128: 70 us against 86 us
+    // one-item and 76 us balanced; 1x8q/1kv x8192x128: 195 against 278 and 235 us),
+    // and head_dim 64 the one-item kernel (1x32x4096x64: 150 us against 160 us split,
+    // 4x32x4096x64: 541 against 582 us). Per-token K/V scales (which the split kernel
+    // does not take) use the one-item kernel; small grids without a workspace, the
+    // split kernel.
     if (sched == REEF_ATTN_SCHED_BALANCED && !stream_ok) return REEF_INVALID_ARGUMENT;
     if (sched == REEF_ATTN_SCHED_SPLIT && tok) return REEF_INVALID_ARGUMENT;
     if (sched == REEF_ATTN_SCHED_BALANCED ||
-        (sched == REEF_ATTN_SCHED_AUTO && stream_ok &&
-         (precise ? items < compute_units() : items <= compute_units()))) {
+        (sched == REEF_ATTN_SCHED_AUTO && stream_ok && items <= compute_units())) {
         const int64_t per_head = host_steps_before(*p, a.q_tiles - 1) +
                                  host_tile_steps(*p, a.q_tiles - 1);
         StreamArgs sa;
@@ -1133,7 +1129,8 @@ extern "C" reef_status reef_attention_prefill_int8(
         return launch_status();
     }
     const bool split = sched == REEF_ATTN_SCHED_SPLIT ||
-                       (sched == REEF_ATTN_SCHED_AUTO && !tok && items <= compute_units());
+                       (sched == REEF_ATTN_SCHED_AUTO && !tok &&
+                        (items <= compute_units() || D == 128));
     // The 4-wave kernel places two workgroups on each of the 256 compute units at
     // once; zig-zag pairs a heavy and a light tile there. The split kernel holds a
     // compute unit alone and takes the tiles heaviest first.
