@@ -262,7 +262,10 @@ struct FlatHeads {
 };
 
 constexpr int kFlatUnroll = 4;
-constexpr int64_t kFlatBlocks = 2048;  // about 8 per compute unit: 128 KB of loads in flight per unit
+// Blocks of a flat launch over `bytes` of input: about 8 per compute unit (128 KB of
+// loads in flight per unit); 4 per unit for streams beyond the cache, which run
+// non-temporal (q, k and v of 4x32x8192x128 per head: 640 against 667 us).
+inline int64_t flat_blocks(int64_t bytes) { return bytes > kStreamBytesTwoPass ? 1024 : 2048; }
 
 __device__ __forceinline__ uint32_t block_max(uint32_t m) {  // the result on thread 0
     __shared__ uint32_t partial[kQuantThreads / kWave];
@@ -664,7 +667,7 @@ extern "C" reef_status reef_quantize_int8_per_tensor(const float *x, int64_t n, 
         f.slice4 = n / 4;
         f.heads = f.batch = 1;
         const int64_t per_slice = std::max<int64_t>(
-            1, std::min<int64_t>(kFlatBlocks, ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
+            1, std::min<int64_t>(flat_blocks(4 * n), ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
         f.chunk4 = ceil_div(f.slice4, per_slice);
         f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
         if (4 * (int64_t)f.blocks <= n) {
@@ -707,7 +710,7 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
     v.tpr = 1;
     while (v.tpr < v.per_row && v.tpr < kQuantThreads) v.tpr *= 2;
     if (vec && v.st == head_dim && batch <= 65535) {
-        // Contiguous tokens: flat float4 streams, about kFlatBlocks blocks in all,
+        // Contiguous tokens: flat float4 streams, about flat_blocks() blocks in all,
         // at least 16 KB of input each; the partial maxima (4 bytes per block) fit
         // in q when q holds at least that many bytes.
         FlatHeads f;
@@ -718,7 +721,8 @@ extern "C" reef_status reef_quantize_int8_per_head(const float *x, int64_t batch
         f.heads = (int32_t)heads;
         f.batch = (int32_t)batch;
         const int64_t per_slice =
-            std::max<int64_t>(1, std::min(ceil_div(kFlatBlocks, batch * heads),
+            std::max<int64_t>(1, std::min(ceil_div(flat_blocks(16 * f.slice4 * batch * heads),
+                                                   batch * heads),
                                           ceil_div(f.slice4, kQuantThreads * kFlatUnroll)));
         f.chunk4 = ceil_div(f.slice4, per_slice);
         f.blocks = (int32_t)ceil_div(f.slice4, f.chunk4);
