@@ -155,12 +155,13 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
  * tune it and for tests that must reach every path. A forced schedule that the
  * call cannot use (BALANCED without a large enough workspace, SPLIT with PER_TOKEN
  * K/V scales, PACKED without head_dim 128, per-tensor or per-head K/V scales and a
- * workspace) returns REEF_INVALID_ARGUMENT. AUTO takes PACKED for head_dim 128 with
- * at least one pair of 256-row query tiles per compute unit (and a workspace that
- * holds the image); BALANCED with a large enough workspace and at most one 128-row
- * query tile per compute unit (fewer than one with PRECISE_PV or PER_TOKEN K/V
- * scales); without a workspace SPLIT for those small grids; ONE_ITEM otherwise.
- * Every schedule splits P into hi + lo where the values need it. */
+ * workspace) returns REEF_INVALID_ARGUMENT, and PACKED outside the packed kernel's
+ * limits REEF_UNSUPPORTED. AUTO takes PACKED for head_dim 128 with at least one
+ * pair of 256-row query tiles per compute unit (and a workspace that holds the
+ * image); BALANCED with a large enough workspace and at most one 128-row query tile
+ * per compute unit; otherwise SPLIT for head_dim 128 and for small grids without a
+ * workspace, ONE_ITEM for head_dim 64 and with PER_TOKEN K/V scales. Every schedule
+ * splits P into hi + lo where the values need it. */
 #define REEF_ATTN_SCHED_MASK 0x70u
 #define REEF_ATTN_SCHED_AUTO 0x00u
 #define REEF_ATTN_SCHED_ONE_ITEM 0x10u /* one 128-row query tile per workgroup */
