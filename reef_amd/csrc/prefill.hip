@@ -5,8 +5,8 @@
 // (batch, head, 128-query tile). Scores are exact int32 sums on the int8
 // matrix cores (v_mfma_i32_32x32x32_i8), dequantized as float(acc) * (s_q * s_k)
 // (the order of operator/linear.hpp:125-127) times softmax_scale, then an fp32
-// online softmax; P.V runs on v_mfma_f32_32x32x16_f16 with P in fp16 (optionally
-// split into hi + lo halves) and the int8 values converted exactly to fp16.
+// online softmax; P.V runs on v_mfma_f32_32x32x16_f16 with P split into fp16 hi + lo
+// parts (22 bits) and the int8 values converted exactly to fp16.
 //
 // Work layout (one workgroup = 4 waves = 128 query rows):
 //   * each wave owns 32 query rows and computes S^T = K . Q^T, so a lane holds
@@ -49,11 +49,12 @@ struct PrefillArgs {
     int32_t zigzag;  // pair heavy and light tiles in grids that fit at once
 };
 
-// Precision of P in a launch: hi + lo parts everywhere, or the choice per item (hi + lo
-// where the item's values reach above kHiOnlyMax, else one fp16 P). One launch holds
-// both bodies, at the hi + lo body's occupancy (one workgroup per SIMD set), rather
-// than one launch per choice, which costs about 5 us where it finds no item.
-constexpr int kPrecHiLo = 1, kPrecPerItem = 2;
+// Precision of P: these kernels always split P into fp16 hi + lo parts (22 bits).
+// Choosing one fp16 P per item, for items whose dequantized values stay within
+// kHiOnlyMax, cost more than it saved: the choice needs the item's value scale
+// before its first tile, and a kernel holding both bodies allocates registers for
+// the larger one (C2 balanced: 71.0 us against 66.4 with hi + lo everywhere), while
+// real heads have values above 1 and take hi + lo anyway.
 
 // Balanced schedule: the steps (item, key tile) of all items, items in (batch,
 // head, query tile) order and each item's tiles in key order, are cut into G
@@ -78,7 +79,7 @@ struct StreamPart {
     int64_t item_u0;  // first step of the item
 };
 
-enum PrefillMode { kWhole = 0, kSplit = 1, kStream = 2 };
+enum PrefillMode { kWhole = 0, kSplit = 1, kStream = 2, kSplitStream = 3 };
 
 template <int D>
 struct StreamSlot {  // floats of one partial result: output in lane order, then (max, sum)
@@ -237,14 +238,17 @@ struct PrefillLds {
 //
 // MODE kWhole and kStream compute key tiles [c0, c1) of the item (kWhole: all of
 // them); kStream parts of a cut item merge through the workspace (StreamArgs).
-template <int D, bool KV_TOKEN, bool PRECISE, int MODE>
+// kSplitStream: the two groups of SPLIT split the key tiles [c0, c1) of a kStream
+// part, merge in LDS, and group 0 goes on as kStream (group 1 joins its barriers).
+template <int D, bool KV_TOKEN, int MODE>
 __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int b, int h, int c0,
                                              int c1, int8_t *smem_all,
                                              float (*sScale)[KV_TOKEN ? 2 * kBN + 1 : 1],
                                              const StreamArgs &sa, const StreamPart &sp,
                                              uint32_t *sTicket) {
-    constexpr bool SPLIT = MODE == kSplit;
-    static_assert(MODE != kSplit || !KV_TOKEN, "the split kernel has no per-token K/V scales");
+    constexpr bool SPLIT = MODE == kSplit || MODE == kSplitStream;
+    constexpr bool STREAM = MODE == kStream || MODE == kSplitStream;
+    static_assert(!SPLIT || !KV_TOKEN, "the split kernels have no per-token K/V scales");
     constexpr int KSTRIDE = PrefillLds<D>::KSTRIDE, VSTRIDE = PrefillLds<D>::VSTRIDE;
     constexpr int DB = D / 32;  // 32-wide output blocks
     constexpr int K_BYTES = PrefillLds<D>::K_BYTES, V_BYTES = PrefillLds<D>::V_BYTES;
@@ -376,9 +380,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     // This group's tiles: [kt0, kt0 + n_tiles * kBN); both groups run n_iter steps.
     int n_iter, kt0, n_tiles;
     if (SPLIT) {
-        n_iter = (n_all + 1) / 2;
-        kt0 = kt_first + (group ? n_iter * kBN : 0);
-        n_tiles = group ? n_all - n_iter : n_iter;
+        const int s0 = MODE == kSplitStream ? c0 : 0;
+        const int n_seg = (MODE == kSplitStream ? min(c1, n_all) : n_all) - s0;
+        n_iter = (n_seg + 1) / 2;
+        kt0 = kt_first + (s0 + (group ? n_iter : 0)) * kBN;
+        n_tiles = group ? n_seg - n_iter : n_iter;
     } else {
         kt0 = kt_first + c0 * kBN;
         n_tiles = min(c1, n_all) - c0;
@@ -505,7 +511,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                             KV_TOKEN ? p * (sScale[buf][kBN + 32 * u + 16 * grp + r] * inv_s) : p;
                         const _Float16 hi16 = (_Float16)pv;
                         phi[u][s][e] = hi16;
-                        if (PRECISE) plo[u][s][e] = (_Float16)(pv - (float)hi16);
+                        plo[u][s][e] = (_Float16)(pv - (float)hi16);
                     }
                     if (!KV_TOKEN) {
                         // Row sum of the fp16 probabilities the P.V product uses, two
@@ -515,10 +521,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
                         for (int e = 0; e < 8; e += 2) {
                             const f16x2 pr = {phi[u][s][e], phi[u][s][e + 1]};
                             l_tile = __builtin_amdgcn_fdot2(pr, one, l_tile, false);
-                            if (PRECISE) {
-                                const f16x2 pl = {plo[u][s][e], plo[u][s][e + 1]};
-                                l_tile = __builtin_amdgcn_fdot2(pl, one, l_tile, false);
-                            }
+                            const f16x2 pl = {plo[u][s][e], plo[u][s][e + 1]};
+                            l_tile = __builtin_amdgcn_fdot2(pl, one, l_tile, false);
                         }
                     }
                 }
@@ -536,7 +540,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
 #pragma unroll
                     for (int d = 0; d < DB; ++d) {
                         acc[d] = mfma_32x32x16_f16(vop[d], phi[u][s], acc[d]);
-                        if (PRECISE) acc[d] = mfma_32x32x16_f16(vop[d], plo[u][s], acc[d]);
+                        acc[d] = mfma_32x32x16_f16(vop[d], plo[u][s], acc[d]);
                     }
                 }
             }
@@ -575,7 +579,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     // q_len (a partial last query tile) compute on zero queries and store nothing.
     const int wg_full_lo = a.window > 0 ? a.query_start + r_last + 1 - a.window : 0;
     const int wg_full_hi = min(a.query_start + q0, a.kv_len - 1);
-    const int it_a = max(0, wg_full_lo - kt0 + kBN - 1) / kBN;
+    // Clamped to n_iter: with a window the first fully visible tile can lie past this
+    // group's tiles, and both groups of a split workgroup must run n_iter steps (one
+    // barrier each).
+    const int it_a = min(n_iter, max(0, wg_full_lo - kt0 + kBN - 1) / kBN);
     const int span = wg_full_hi + 1 - kt0;  // keys from kt0 through wg_full_hi
     const int it_b = max(it_a, min(n_tiles, span > 0 ? span / kBN : 0));
 
@@ -603,7 +610,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             xml[wave * kWave + lane] = float2{m_run, l_tot};
         }
         __syncthreads();
-        if (group == 1) return;
+        if (group == 1) {
+            // the two barriers of group 0's part store and count below
+            if (MODE == kSplitStream && sp.parts > 1) {
+                __syncthreads();
+                __syncthreads();
+            }
+            return;
+        }
         const float2 other = xml[wave * kWave + lane];
         const float m = fmaxf(m_run, other.x);
         const float w0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
@@ -617,6 +631,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[d][4 * j + i] = acc[d][4 * j + i] * w0 + o[i] * w1;
             }
+        m_run = m;  // the merged state's maximum (a kSplitStream part stores it)
     }
     if (KV_TOKEN && MODE == kStream) {
         // Parts merge in absolute value units: the accumulator leaves the units of
@@ -627,7 +642,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
             for (int i = 0; i < 16; ++i) acc[d][i] *= s_run * (1.0f / 64.0f);
         s_run = 64.0f;
     }
-    if (MODE == kStream && sp.parts > 1) {
+    if (STREAM && sp.parts > 1) {
         // Leave this part in its slot (every lane: rows past q_len hold finite
         // values), then count the part in; the last part of the item merges. Every
         // access to a slot is a device-coherent atomic (agent scope: written through
@@ -673,7 +688,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
         // Every part, this one included, comes from its slot, folded in part order (a
         // running log-sum-exp with explicit fused multiply-adds: the same roundings
         // whichever part merges), kMergeAhead parts' loads in flight at a time.
-        constexpr int kMergeAhead = KV_TOKEN || PRECISE ? 2 : 1;
+        constexpr int kMergeAhead = 2;
         float m = -INFINITY, l = 0.0f;
         f32x16 tot[DB];
 #pragma unroll
@@ -731,19 +746,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs &a, int tile, int
     }
 }
 
-// Whether the values of (batch b, query head h)'s kv head reach above kHiOnlyMax
-// (per-tensor or per-head value scales): such items take P split into hi + lo.
-__device__ __forceinline__ bool item_is_wide(const PrefillArgs &a, int b, int h) {
-    const int kvh = h / (a.q_heads / a.kv_heads);
-    return 127.0f * scale_of(a.vs, a.kv_gran, b, kvh, 0, a.kv_heads, a.kv_len) > kHiOnlyMax;
-}
-
 // Persistent form of the split kernel: one workgroup per compute unit takes the
 // items of round r = 0, 1, ... at index r * G + blockIdx.x, the odd rounds in
 // reverse order, so that with heaviest-first ranks every workgroup's sum of work
 // is about the same. A workgroup's next item starts while the stores of its last
 // one drain.
-template <int D, int PREC>
+template <int D>
 __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillArgs a, int items) {
     static_assert(4 * (D / 32) * 4 * kWave * 16 + 4 * kWave * 8 <= 2 * PrefillLds<D>::BYTES,
                   "merge buffer fits in the stages");
@@ -758,38 +766,36 @@ __global__ __launch_bounds__(2 * kThreads, 1) void prefill_split_kernel(PrefillA
         }
         int tile, b, h;
         item_coords(a, item, tile, b, h);
-        if (PREC == kPrecHiLo || (PREC == kPrecPerItem && item_is_wide(a, b, h)))  // uniform
-            prefill_body<D, false, true, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
-                                                 StreamPart{}, nullptr);
-        else
-            prefill_body<D, false, false, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
-                                                  StreamPart{}, nullptr);
+        prefill_body<D, false, kSplit>(a, tile, b, h, 0, 0, smem, sScale, StreamArgs{},
+                                       StreamPart{}, nullptr);
         __syncthreads();  // the next item's stages overwrite the merge buffer
     }
 }
 
-template <int D, bool KV_TOKEN, int PREC>
+template <int D, bool KV_TOKEN>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
     int tile, b, h;
     item_coords(a, grid_rank(a), tile, b, h);
-    if (KV_TOKEN || PREC == kPrecHiLo || (PREC == kPrecPerItem && item_is_wide(a, b, h)))
-        prefill_body<D, KV_TOKEN, true, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
-                                                StreamArgs{}, StreamPart{}, nullptr);
-    else
-        prefill_body<D, KV_TOKEN, false, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale,
-                                                 StreamArgs{}, StreamPart{}, nullptr);
+    prefill_body<D, KV_TOKEN, kWhole>(a, tile, b, h, 0, INT32_MAX, smem, sScale, StreamArgs{},
+                                      StreamPart{}, nullptr);
 }
 
 // Balanced schedule (StreamArgs): workgroup g works through the steps
 // [L G^-1 units, (L + 1) G^-1 units) of logical workgroup L, where the G / 8
 // workgroups that run on one XCD (hardware workgroup g goes to XCD g % 8) hold
-// consecutive L, so an XCD's L2 sees a few heads, not all of them.
-template <int D, bool KV_TOKEN, int PREC>
-__global__ __launch_bounds__(kThreads, 1) void prefill_stream_kernel(
+// consecutive L, so an XCD's L2 sees a few heads, not all of them. GROUPS 2: the
+// workgroup is two 4-wave groups that split each part's key tiles (kSplitStream).
+template <int D, bool KV_TOKEN, int GROUPS>
+__global__ __launch_bounds__(GROUPS * kThreads, 1) void prefill_stream_kernel(
     PrefillArgs a, StreamArgs sa) {
-    __shared__ __attribute__((aligned(16))) int8_t smem[PrefillLds<D>::BYTES];
+    static_assert(GROUPS == 1 || (GROUPS == 2 && !KV_TOKEN), "two groups: no per-token scales");
+    static_assert(GROUPS == 1 || 4 * (D / 32) * 4 * kWave * 16 + 4 * kWave * 8 <=
+                                     2 * PrefillLds<D>::BYTES,
+                  "merge buffer fits in the stages");
+    constexpr int MODE = GROUPS == 2 ? kSplitStream : kStream;
+    __shared__ __attribute__((aligned(16))) int8_t smem[GROUPS * PrefillLds<D>::BYTES];
     __shared__ float sScale[2][KV_TOKEN ? 2 * kBN + 1 : 1];
     __shared__ uint32_t sTicket;
     const int G = gridDim.x, g = blockIdx.x;
@@ -824,14 +830,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_stream_kernel(
         sp.parts = wg_of(sp.item_u0 + n - 1) - sp.first_wg + 1;
         sp.slot = 2 * L + (first ? 0 : 1);
         sp.item = bh * a.q_tiles + tile;
-        // Every part of an item takes the same precision (a function of the item).
-        if (KV_TOKEN || PREC == kPrecHiLo ||
-            (PREC == kPrecPerItem && item_is_wide(a, bh / a.q_heads, bh % a.q_heads)))
-            prefill_body<D, KV_TOKEN, true, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0,
-                                                     c1, smem, sScale, sa, sp, &sTicket);
-        else
-            prefill_body<D, KV_TOKEN, false, kStream>(a, tile, bh / a.q_heads, bh % a.q_heads, c0,
-                                                      c1, smem, sScale, sa, sp, &sTicket);
+        prefill_body<D, KV_TOKEN, MODE>(a, tile, bh / a.q_heads, bh % a.q_heads, c0, c1, smem,
+                                        sScale, sa, sp, &sTicket);
         u += c1 - c0;
         c0 = 0;
         first = false;
@@ -917,7 +917,7 @@ int64_t stream_groups() { return 2 * compute_units(); }
 constexpr int64_t kCounterWords = 65536;
 constexpr int64_t kQueueWords = 16;  // the last words: the packed schedule's item queue
 constexpr int64_t kStreamMaxItems = kCounterWords - kQueueWords;
-constexpr int64_t kStreamMinSteps = 8;  // steps per workgroup of the precise balanced kernels
+constexpr int64_t kStreamMinSteps = 8;  // steps per workgroup of the balanced kernels
 constexpr int64_t kStreamCounterBytes = kCounterWords * 4;
 
 int64_t stream_items(const reef_attention_params &p) {
@@ -1035,10 +1035,6 @@ extern "C" reef_status reef_attention_prefill_int8(
     if (items >= (int64_t(1) << 31)) return REEF_UNSUPPORTED;
     const dim3 grid((unsigned)items);
     const bool tok = p->kv_granularity == REEF_SCALE_PER_TOKEN;
-    // Per-token K/V scales fold the value scale into P (p * s_v / max s_v) before its
-    // fp16 rounding, which no longer cancels against the row sum; those launches
-    // always split P into fp16 hi + lo parts to stay well inside the tolerance.
-    const bool precise = (p->flags & REEF_ATTN_PRECISE_PV) != 0 || tok;
     if (workspace && !aligned(workspace, 256)) return REEF_INVALID_ARGUMENT;
     const uint32_t sched = p->flags & REEF_ATTN_SCHED_MASK;
     if (sched != REEF_ATTN_SCHED_AUTO && sched != REEF_ATTN_SCHED_ONE_ITEM &&
@@ -1109,23 +1105,23 @@ extern "C" reef_status reef_attention_prefill_int8(
         const dim3 sgrid((unsigned)std::min<int64_t>(
             std::max<int64_t>(1, std::min<int64_t>(compute_units(), sa.units / kStreamMinSteps)),
             sa.units));
-#define REEF_STREAM_LAUNCH(DIM, TOK, PREC)                                                 \
-    hipLaunchKernelGGL((prefill_stream_kernel<DIM, TOK, PREC>), sgrid, dim3(kThreads), 0, \
-                       stream, a, sa)
-        // One launch: hi + lo P everywhere (the precision flag, per-token K/V scales)
-        // or per item, on the precise kernels' grid (items whose values stay within
-        // kHiOnlyMax, which take one fp16 P, are rare in practice).
+        // Per-token K/V scales: one 4-wave group per workgroup; otherwise two groups
+        // that split each part's key tiles (two waves per SIMD).
         if (tok) {
-            if (D == 128) REEF_STREAM_LAUNCH(128, true, kPrecHiLo);
-            else REEF_STREAM_LAUNCH(64, true, kPrecHiLo);
-        } else if (precise) {
-            if (D == 128) REEF_STREAM_LAUNCH(128, false, kPrecHiLo);
-            else REEF_STREAM_LAUNCH(64, false, kPrecHiLo);
+            if (D == 128)
+                hipLaunchKernelGGL((prefill_stream_kernel<128, true, 1>), sgrid, dim3(kThreads), 0,
+                                   stream, a, sa);
+            else
+                hipLaunchKernelGGL((prefill_stream_kernel<64, true, 1>), sgrid, dim3(kThreads), 0,
+                                   stream, a, sa);
         } else {
-            if (D == 128) REEF_STREAM_LAUNCH(128, false, kPrecPerItem);
-            else REEF_STREAM_LAUNCH(64, false, kPrecPerItem);
+            if (D == 128)
+                hipLaunchKernelGGL((prefill_stream_kernel<128, false, 2>), sgrid,
+                                   dim3(2 * kThreads), 0, stream, a, sa);
+            else
+                hipLaunchKernelGGL((prefill_stream_kernel<64, false, 2>), sgrid,
+                                   dim3(2 * kThreads), 0, stream, a, sa);
         }
-#undef REEF_STREAM_LAUNCH
         return launch_status();
     }
     const bool split = sched == REEF_ATTN_SCHED_SPLIT ||
@@ -1137,30 +1133,22 @@ extern "C" reef_status reef_attention_prefill_int8(
     a.zigzag = !split && items <= 2 * compute_units() ? 1 : 0;
     if (split) {
         const dim3 pgrid((unsigned)std::min<int64_t>(items, compute_units()));
-#define REEF_SPLIT_LAUNCH(DIM, PREC)                                                         \
-    hipLaunchKernelGGL((prefill_split_kernel<DIM, PREC>), pgrid, dim3(2 * kThreads), 0, stream, a, \
-                       (int)items)
-        if (precise) {
-            if (D == 128) REEF_SPLIT_LAUNCH(128, kPrecHiLo);
-            else REEF_SPLIT_LAUNCH(64, kPrecHiLo);
-        } else {  // one fp16 P or hi + lo per item, in one launch
-            if (D == 128) REEF_SPLIT_LAUNCH(128, kPrecPerItem);
-            else REEF_SPLIT_LAUNCH(64, kPrecPerItem);
-        }
-#undef REEF_SPLIT_LAUNCH
+        if (D == 128)
+            hipLaunchKernelGGL(prefill_split_kernel<128>, pgrid, dim3(2 * kThreads), 0, stream, a,
+                               (int)items);
+        else
+            hipLaunchKernelGGL(prefill_split_kernel<64>, pgrid, dim3(2 * kThreads), 0, stream, a,
+                               (int)items);
         return launch_status();
     }
-#define REEF_PREFILL_LAUNCH(DIM, TOK, PREC)                                                  \
-    hipLaunchKernelGGL((prefill_kernel<DIM, TOK, PREC>), grid, dim3(kThreads), 0, stream, a)
-    if (tok) {  // per-token K/V scales always split P
-        if (D == 128) REEF_PREFILL_LAUNCH(128, true, kPrecHiLo);
-        else REEF_PREFILL_LAUNCH(64, true, kPrecHiLo);
-    } else if (precise) {
-        if (D == 128) REEF_PREFILL_LAUNCH(128, false, kPrecHiLo);
-        else REEF_PREFILL_LAUNCH(64, false, kPrecHiLo);
-    } else {  // one fp16 P or hi + lo per item, in one launch
-        if (D == 128) REEF_PREFILL_LAUNCH(128, false, kPrecPerItem);
-        else REEF_PREFILL_LAUNCH(64, false, kPrecPerItem);
+#define REEF_PREFILL_LAUNCH(DIM, TOK) \
+    hipLaunchKernelGGL((prefill_kernel<DIM, TOK>), grid, dim3(kThreads), 0, stream, a)
+    if (tok) {
+        if (D == 128) REEF_PREFILL_LAUNCH(128, true);
+        else REEF_PREFILL_LAUNCH(64, true);
+    } else {
+        if (D == 128) REEF_PREFILL_LAUNCH(128, false);
+        else REEF_PREFILL_LAUNCH(64, false);
     }
 #undef REEF_PREFILL_LAUNCH
     return launch_status();
