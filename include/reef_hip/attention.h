@@ -142,11 +142,12 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
 
 /* Attention flags. */
 #define REEF_ATTN_PRECISE_PV 0x1u /* P.V with P split into fp16 hi + lo parts (22
-                                     * bits) whatever the values. Without it the split
-                                     * applies wherever a head's dequantized values reach
-                                     * above 1 in magnitude (always with PER_TOKEN K/V
-                                     * scales); at or below 1 one fp16 P moves an output
-                                     * by at most 2^-11 max|v_j - out| <= 9.8e-4. Either
+                                     * bits) whatever the values. Without it the packed
+                                     * schedule splits wherever a head's dequantized
+                                     * values reach above 1 in magnitude, the other
+                                     * schedules always; at or below 1 one fp16 P moves
+                                     * an output by at most 2^-11 max|v_j - out| <=
+                                     * 9.8e-4. Either
                                      * way each P carries an exponent offset that keeps
                                      * it out of the fp16 subnormals, so small weights
                                      * keep their precision */
@@ -166,12 +167,11 @@ reef_status reef_gemm_w8a8(const int8_t *xq, const float *x_scales, int64_t rows
 #define REEF_ATTN_SCHED_AUTO 0x00u
 #define REEF_ATTN_SCHED_ONE_ITEM 0x10u /* one 128-row query tile per workgroup */
 #define REEF_ATTN_SCHED_SPLIT 0x20u    /* persistent workgroups; two 4-wave groups split
-                                        * each tile's keys; hi + lo P where the values
-                                        * need it or with PRECISE_PV */
-#define REEF_ATTN_SCHED_BALANCED 0x30u /* equal (tile, key block) ranges per workgroup;
-                                        * cut tiles merge through the workspace; hi + lo
-                                        * P where the values need it or with PRECISE_PV
-                                        * or PER_TOKEN K/V scales */
+                                        * each tile's keys; hi + lo P */
+#define REEF_ATTN_SCHED_BALANCED 0x30u /* equal (tile, key block) ranges per workgroup,
+                                        * two 4-wave groups splitting each range's key
+                                        * tiles (one with PER_TOKEN K/V scales); cut
+                                        * tiles merge through the workspace; hi + lo P */
 #define REEF_ATTN_SCHED_PACKED 0x40u   /* head_dim 128, per-tensor / per-head K and V
                                         * scales: V packed once into an fp16 image in the
                                         * workspace, 128-row query tiles, persistent
