@@ -200,8 +200,8 @@ def prefill_kernels(torch, cfg):
     attention kernel) when head_dim is 128 and there is at least one pair of 256-row
     query tiles per compute unit; the balanced schedule with at most one 128-row
     query tile per compute unit; otherwise the split kernel at head_dim 128 and the
-    one-item kernel at 64. Each is one launch, which splits P into fp16 hi + lo parts
-    for the items whose values need it."""
+    one-item kernel at 64. Each is one launch; the packed kernel splits P into fp16
+    hi + lo parts for the heads whose values need it, the others always."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     pairs = ((cfg.seq + 255) // 256 + 1) // 2 * cfg.batch * cfg.q_heads
     if cfg.head_dim == 128 and pairs >= cus:
