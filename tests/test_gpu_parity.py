@@ -326,6 +326,10 @@ PREFILL_CASES = [
     (1, 4, 2, 300, 700, 128, 250, 90, 1, 1, None),
     # several 256-row query tiles and an odd tile count (a middle tile without a pair)
     (2, 3, 3, 1200, 1200, 128, None, 0, 1, 1, None),
+    # a window shorter than a query tile on a grid of many tiles: the first fully
+    # visible key tile lies past the second group's tiles of a split workgroup, whose
+    # two groups must still run the same number of steps
+    (1, 4, 2, 1200, 1200, 128, None, 100, 1, 1, None),
 ]
 
 
