@@ -53,8 +53,8 @@ struct PrefillArgs {
 // Choosing one fp16 P per item, for items whose dequantized values stay within
 // kHiOnlyMax, cost more than it saved: the choice needs the item's value scale
 // before its first tile, and a kernel holding both bodies allocates registers for
-// the larger one (C2 balanced: 71.0 us against 66.4 with hi + lo everywhere), while
-// real heads have values above 1 and take hi + lo anyway.
+// the larger one (1x32x2048x128 balanced: 71.0 us against 66.4 with hi + lo
+// everywhere), while real heads have values above 1 and take hi + lo anyway.
 
 // Balanced schedule: the steps (item, key tile) of all items, items in (batch,
 // head, query tile) order and each item's tiles in key order, are cut into G
@@ -1071,15 +1071,13 @@ extern "C" reef_status reef_attention_prefill_int8(
         return prefill_packed_launch(p, q, qst, k, kst, v, vst, q_scales, k_scales, v_scales, out,
                                      ost, static_cast<char *>(workspace) + bal_bytes, work, stream);
     }
-    // Every schedule splits P into hi + lo where the values need it: always with the
-    // precision flag or per-token K/V scales, otherwise per item, in one launch. The
-    // library takes the balanced schedule, which cuts the causal work of all items
-    // into equal ranges, for grids of at most one 128-row tile per compute unit
-    // (1x8q/1kv x4096x128: 71 us against 86 us with the split kernel and 101 us with
-    // the one-item kernel; 69 against 84 and 97 us with the precision flag). On
-    // larger grids, head_dim 128 takes the split kernel, whose two 4-wave groups per
-    // workgroup halve each tile's key loop (1x32x2048x128: 70 us against 86 us
-    // one-item and 76 us balanced; 1x8q/1kv x8192x128: 195 against 278 and 235 us),
+    // The library takes the balanced schedule, which cuts the causal work of all
+    // items into equal ranges, for grids of at most one 128-row tile per compute unit
+    // (1x8q/1kv x4096x128: 63.6 us against 81.6 us with the split kernel and 92.5 us
+    // with the one-item kernel). On larger grids, head_dim 128 takes the split
+    // kernel, whose two 4-wave groups per workgroup halve each tile's key loop
+    // (1x32x2048x128: 65.9 us against 82.0 us one-item and 66.0 us balanced;
+    // 1x8q/1kv x8192x128: 195 against 278 us one-item),
     // and head_dim 64 the one-item kernel (1x32x4096x64: 150 us against 160 us split,
     // 4x32x4096x64: 541 against 582 us). Per-token K/V scales (which the split kernel
     // does not take) use the one-item kernel; small grids without a workspace, the

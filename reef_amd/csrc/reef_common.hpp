@@ -20,11 +20,12 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.44269504088896341f;
-// P.V precision: where dequantized values reach above this magnitude, P is split
-// into fp16 hi + lo parts (22 bits). Below it one fp16 P, each off by at most 2^-11
-// of itself, moves an output by at most 2^-11 max|v_j - out| <= 2^-11 * 2 = 9.8e-4,
-// inside the 1e-3 attention tolerance for every input (REEF_ATTN_PRECISE_PV splits
-// every block whatever the values).
+// P.V precision of the packed prefill: where a head's dequantized values reach above
+// this magnitude, P is split into fp16 hi + lo parts (22 bits). Below it one fp16 P,
+// each off by at most 2^-11 of itself, moves an output by at most
+// 2^-11 max|v_j - out| <= 2^-11 * 2 = 9.8e-4, inside the 1e-3 attention tolerance for
+// every input (REEF_ATTN_PRECISE_PV splits every head whatever the values; the other
+// prefill kernels and decode always split).
 constexpr float kHiOnlyMax = 1.0f;
 
 // --- matrix instructions ---------------------------------------------------------------
